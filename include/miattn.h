@@ -1,0 +1,166 @@
+/*
+ * miattn.h — C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Every entry point takes raw device pointers, element strides (int64, in
+ * elements, not bytes), a dtype code and the hipStream_t to launch on (as
+ * void*).  Nothing here allocates, frees or synchronises: outputs and
+ * workspaces are owned by the caller (the Python layer takes them from
+ * torch's caching allocator, which keeps every call legal under hipGraph
+ * capture).  Launch geometry depends only on shapes and capacities, never
+ * on device-resident values, so captured graphs stay valid across replays.
+ *
+ * Return value: 0 on success; negative = invalid argument / unsupported
+ * shape (nothing was launched); positive = hipError_t reported by the
+ * runtime right after the launch.  mi_last_error() returns a description of
+ * the most recent failure on the calling thread.
+ *
+ * Reference interfaces (Analysis196884/llm-infer-engine) each entry point
+ * replaces are cited next to it as path:line.
+ */
+#ifndef MIATTN_H_
+#define MIATTN_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes */
+#define MI_DTYPE_BF16 0
+#define MI_DTYPE_F16 1
+#define MI_DTYPE_F32 2
+
+/* status codes */
+#define MI_OK 0
+#define MI_ERR_INVALID -1     /* bad pointer / shape / stride / alignment */
+#define MI_ERR_UNSUPPORTED -2 /* valid request this build has no kernel for */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int32_t mi_version(void);
+
+/* Description of the last failure on this thread ("" if none). */
+const char* mi_last_error(void);
+
+/*
+ * Split-KV single-token decode, phase 1: per (batch, kv-head, split) partial
+ * softmax state for ALL query heads of the GQA group (each KV byte is read
+ * once per group, not once per query head).
+ *
+ * Replaces _flash_decode_split_kernel + its launch
+ *   src/flash_decode.py:8-137, src/flash_decode.py:300-342.
+ *
+ * q        [batch, n_heads, 1, head_dim]      strides (q_sb, q_sh, q_sd)
+ * k, v     [batch, n_kv_heads, kv_len, head_dim], innermost stride 1,
+ *          rows 16-byte aligned                strides (*_sb, *_sh, *_sl)
+ * mask     optional bool bytes; key j of batch b participates iff
+ *          mask[b*mask_sb + j*mask_sl] != 0 (mask_sb = 0 broadcasts)
+ *          (src/flash_decode.py:87-95, :215-233)
+ * seq_lens optional int64 [batch] on device: keys j >= seq_lens[b] are
+ *          neither read nor counted (graph-safe variable lengths)
+ * part_m, part_l  fp32 [batch, n_heads, num_splits]      (contiguous)
+ * part_acc        fp32 [batch, n_heads, num_splits, head_dim] (contiguous)
+ *          part_m holds the running max of the scaled scores in log2 units;
+ *          part_l/part_acc the matching sum / unnormalised accumulator.
+ *          An empty split stores l = 0 (src/flash_decode.py:97-99,131-137).
+ * Keys are split into num_splits contiguous ranges of ceil(kv_len/num_splits).
+ */
+int32_t mi_decode_split(const void* q, const void* k, const void* v,
+                        const uint8_t* mask, int64_t mask_sb, int64_t mask_sl,
+                        const int64_t* seq_lens, float* part_m, float* part_l,
+                        float* part_acc, int64_t batch, int64_t n_heads,
+                        int64_t n_kv_heads, int64_t kv_len, int64_t head_dim,
+                        int64_t num_splits, int64_t q_sb, int64_t q_sh,
+                        int64_t q_sd, int64_t k_sb, int64_t k_sh, int64_t k_sl,
+                        int64_t v_sb, int64_t v_sh, int64_t v_sl,
+                        float sm_scale, int32_t dtype, void* stream);
+
+/*
+ * Split-KV decode, phase 2: log-sum-exp combine of the partials.
+ * Replaces _flash_decode_reduce_kernel + its launch
+ *   src/flash_decode.py:140-212, src/flash_decode.py:344-369.
+ *
+ * out [batch, n_heads, 1, head_dim] (strides o_sb, o_sh, o_sd), dtype of q.
+ * lse optional fp32 [batch, n_heads] (natural log of the scaled scores).
+ * Rows with no participating key produce 0 (src/flash_decode.py:204-205),
+ * or NaN when empty_rows_nan != 0 (the 0/0 of src/decode_attn.py:70), and
+ * lse = -inf.
+ */
+int32_t mi_decode_combine(const float* part_m, const float* part_l,
+                          const float* part_acc, void* out, float* lse,
+                          int64_t batch, int64_t n_heads, int64_t head_dim,
+                          int64_t num_splits, int64_t o_sb, int64_t o_sh,
+                          int64_t o_sd, int32_t empty_rows_nan, int32_t dtype,
+                          void* stream);
+
+/*
+ * Both decode phases in one call (what flash_decode / decode_attention use).
+ * With num_splits == 1 the partial buffers may be NULL: the split kernel then
+ * normalises and writes out/lse itself (single launch).
+ * Replaces flash_decode() src/flash_decode.py:236-370 and
+ * decode_attention() src/decode_attn.py:137-166.
+ */
+int32_t mi_flash_decode(const void* q, const void* k, const void* v,
+                        const uint8_t* mask, int64_t mask_sb, int64_t mask_sl,
+                        const int64_t* seq_lens, float* part_m, float* part_l,
+                        float* part_acc, void* out, float* lse, int64_t batch,
+                        int64_t n_heads, int64_t n_kv_heads, int64_t kv_len,
+                        int64_t head_dim, int64_t num_splits, int64_t q_sb,
+                        int64_t q_sh, int64_t q_sd, int64_t k_sb, int64_t k_sh,
+                        int64_t k_sl, int64_t v_sb, int64_t v_sh, int64_t v_sl,
+                        int64_t o_sb, int64_t o_sh, int64_t o_sd,
+                        float sm_scale, int32_t empty_rows_nan, int32_t dtype,
+                        void* stream);
+
+/*
+ * Split count the library would pick for a decode of this shape on the
+ * current device (used when the caller passes no explicit num_splits).
+ */
+int64_t mi_decode_default_splits(int64_t batch, int64_t n_heads,
+                                 int64_t n_kv_heads, int64_t kv_len,
+                                 int64_t head_dim);
+
+/*
+ * Rotate-half RoPE of x [batch, n_heads, seq_len, head_dim] into out (any
+ * strides).  Row s uses cos/sin row s of the [seq_len, head_dim/2] tables
+ * (the caller slices the table at start_pos).  cdtype is the table dtype.
+ * Replaces rope_kernel + apply_rotary  src/rope.py:48-91, src/rope.py:94-119.
+ */
+int32_t mi_rope(const void* x, void* out, const void* cos, const void* sin,
+                int64_t batch, int64_t n_heads, int64_t seq_len,
+                int64_t head_dim, int64_t x_sb, int64_t x_sh, int64_t x_ss,
+                int64_t x_sd, int64_t o_sb, int64_t o_sh, int64_t o_ss,
+                int64_t o_sd, int64_t c_ss, int64_t c_sd, int64_t s_ss,
+                int64_t s_sd, int32_t dtype, int32_t cdtype, void* stream);
+
+/*
+ * Fused K-RoPE + KV-cache append: cache_k[b, h, pos] = RoPE(xk[b, h, s]) and
+ * cache_v[b, h, pos] = xv[b, h, s] (bitwise copy), with
+ * pos = start_pos + s, or pos = positions[s] (device int64, one position per
+ * token shared by the batch) when positions != NULL.  cache_k/cache_v point
+ * at the layer view [batch, n_kv_heads, capacity, head_dim]; slots outside
+ * [0, capacity) are never written.  cos/sin rows are indexed by s, or by pos
+ * when cos_by_position != 0 (device-resident full table).  With cos = sin =
+ * NULL, K is copied unrotated (plain cache write, KVCache.update).
+ * Replaces _rope_k_cache_write_seq_kernel / _scatter_kernel +
+ * rope_and_cache_update  src/rope.py:122-252, src/rope.py:255-313.
+ */
+int32_t mi_rope_kv_append(const void* xk, const void* xv, const void* cos,
+                          const void* sin, void* cache_k, void* cache_v,
+                          int64_t start_pos, const int64_t* positions,
+                          int64_t batch, int64_t n_kv_heads, int64_t seq_len,
+                          int64_t head_dim, int64_t capacity, int64_t xk_sb,
+                          int64_t xk_sh, int64_t xk_ss, int64_t xk_sd,
+                          int64_t xv_sb, int64_t xv_sh, int64_t xv_ss,
+                          int64_t xv_sd, int64_t ck_sb, int64_t ck_sh,
+                          int64_t ck_st, int64_t ck_sd, int64_t cv_sb,
+                          int64_t cv_sh, int64_t cv_st, int64_t cv_sd,
+                          int64_t c_ss, int64_t c_sd, int64_t s_ss,
+                          int64_t s_sd, int32_t cos_by_position, int32_t dtype,
+                          int32_t cdtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MIATTN_H_ */

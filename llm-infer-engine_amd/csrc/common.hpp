@@ -1,0 +1,132 @@
+// Shared device helpers for the gfx950 attention-path kernels.
+//
+// Everything here is written for CDNA4 (gfx950): 64-lane wavefronts, DPP
+// row operations for intra-row reductions, 16-byte vector memory accesses.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/miattn.h"
+
+namespace mi {
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+// Floor for running maxima (log2 domain).  Keeps "empty" state finite so the
+// online-softmax rescale never evaluates (-inf) - (-inf).
+constexpr float kNegBig = -1.0e30f;
+
+// ---------------------------------------------------------------- host side
+void set_last_error(const char* fmt, ...);
+
+// ---------------------------------------------------------- element traits
+template <typename T> struct Elem;
+template <> struct Elem<bf16_t> {
+  static constexpr int kBytes = 2;
+  __device__ static inline float to_f32(bf16_t x) { return (float)x; }
+  __device__ static inline bf16_t from_f32(float x) { return (bf16_t)x; }
+};
+template <> struct Elem<f16_t> {
+  static constexpr int kBytes = 2;
+  __device__ static inline float to_f32(f16_t x) { return (float)x; }
+  __device__ static inline f16_t from_f32(float x) { return (f16_t)x; }
+};
+template <> struct Elem<float> {
+  static constexpr int kBytes = 4;
+  __device__ static inline float to_f32(float x) { return x; }
+  __device__ static inline float from_f32(float x) { return x; }
+};
+
+// Unpack one 16-byte chunk into fp32 values (8 for 2-byte types, 4 for fp32).
+template <typename T> struct Chunk;
+template <> struct Chunk<bf16_t> {
+  static constexpr int kN = 8;
+  __device__ static inline void unpack(const u32x4& w, float* o) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[2 * i] = __uint_as_float(u[i] << 16);
+      o[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+    }
+  }
+};
+template <> struct Chunk<f16_t> {
+  static constexpr int kN = 8;
+  __device__ static inline void unpack(const u32x4& w, float* o) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      union { uint32_t u; f16_t h[2]; } c;
+      c.u = u[i];
+      o[2 * i] = (float)c.h[0];
+      o[2 * i + 1] = (float)c.h[1];
+    }
+  }
+};
+template <> struct Chunk<float> {
+  static constexpr int kN = 4;
+  __device__ static inline void unpack(const u32x4& w, float* o) {
+    o[0] = __uint_as_float(w.x);
+    o[1] = __uint_as_float(w.y);
+    o[2] = __uint_as_float(w.z);
+    o[3] = __uint_as_float(w.w);
+  }
+};
+
+// ------------------------------------------------------------- DPP helpers
+template <int CTRL>
+__device__ inline float dpp_f32(float x) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// Sum over aligned groups of N lanes (N in {1,2,4,8,16}); every lane of the
+// group receives the total.  Uses only intra-row DPP (no LDS traffic).
+template <int N>
+__device__ inline float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp_f32<0xB1>(x);   // quad_perm [1,0,3,2]
+  if constexpr (N >= 4) x += dpp_f32<0x4E>(x);   // quad_perm [2,3,0,1]
+  if constexpr (N >= 8) x += dpp_f32<0x141>(x);  // row_half_mirror
+  if constexpr (N >= 16) x += dpp_f32<0x140>(x); // row_mirror
+  return x;
+}
+
+template <int N>
+__device__ inline float group_max(float x) {
+  if constexpr (N >= 2) x = fmaxf(x, dpp_f32<0xB1>(x));
+  if constexpr (N >= 4) x = fmaxf(x, dpp_f32<0x4E>(x));
+  if constexpr (N >= 8) x = fmaxf(x, dpp_f32<0x141>(x));
+  if constexpr (N >= 16) x = fmaxf(x, dpp_f32<0x140>(x));
+  return x;
+}
+
+__device__ inline float shfl_xor_f32(float x, int mask) {
+  return __shfl_xor(x, mask, 64);
+}
+
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+__device__ inline u32x4 load16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+// Streaming (read-once) 16-byte load: non-temporal hint so KV bytes that are
+// read exactly once do not evict reusable lines from L2.
+__device__ inline u32x4 load16_stream(const void* p) {
+  const u32x4* q = reinterpret_cast<const u32x4*>(p);
+  return __builtin_nontemporal_load(q);
+}
+
+}  // namespace mi

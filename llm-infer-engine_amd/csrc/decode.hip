@@ -1,0 +1,780 @@
+// Split-KV single-token decode attention for gfx950 (bandwidth-bound path).
+//
+// Math follows the reference's split/combine decode
+// (src/flash_decode.py:8-137 per-split partials, :140-212 LSE combine), but the
+// work decomposition is MI355X-first:
+//   * one workgroup per (batch, kv-head, split) computes the partial state of
+//     ALL query heads that share the kv-head (GQA), so every K/V byte is read
+//     from HBM exactly once (the reference re-reads it once per query head);
+//   * each lane owns one 16-byte chunk of a K/V row per load (coalesced
+//     128-bit global loads; a row of D elements spans LPR = D*sizeof(T)/16
+//     lanes, capped at 16 = one DPP row);
+//   * q.k row sums use DPP row reductions (no LDS round trip), the softmax is
+//     kept per 16-lane row group in registers (log2 domain, v_exp_f32), and the
+//     groups/waves are merged once at the end through LDS;
+//   * no MFMA: at one query token per head there is nothing to amortise a
+//     matrix tile over, and the loop is HBM-bound.
+// Keys beyond seq_lens[b] are never loaded (the grid is static so the launch
+// is hipGraph-safe; surplus splits just publish an empty partial).
+#include <math.h>
+
+#include <algorithm>
+
+#include "common.hpp"
+
+namespace mi {
+
+struct DecodeArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const uint8_t* mask;
+  int64_t mask_sb, mask_sl;
+  const int64_t* seq_lens;
+  float* part_m;
+  float* part_l;
+  float* part_acc;
+  void* out;
+  float* lse;
+  int64_t q_sb, q_sh, q_sd;
+  int64_t k_sb, k_sh, k_sl;
+  int64_t v_sb, v_sh, v_sl;
+  int64_t o_sb, o_sh, o_sd;
+  int32_t n_heads, group, kv_len;
+  int32_t split_len, num_splits, n_chunks, chunk_heads;
+  float scale_log2;
+  int32_t direct;     // num_splits == 1: normalise and write out/lse here
+  int32_t empty_nan;  // empty rows -> NaN instead of 0
+  int32_t q_vec;      // q rows are 16-byte aligned with unit d-stride
+};
+
+// q.k over one 16-byte chunk, fp32 accumulate.
+template <typename T>
+__device__ inline float dot_chunk(const u32x4& q, const u32x4& k, float acc);
+
+template <>
+__device__ inline float dot_chunk<bf16_t>(const u32x4& q, const u32x4& k,
+                                          float acc) {
+  const uint32_t qa[4] = {q.x, q.y, q.z, q.w};
+  const uint32_t ka[4] = {k.x, k.y, k.z, k.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    bf16x2 a = __builtin_bit_cast(bf16x2, qa[i]);
+    bf16x2 b = __builtin_bit_cast(bf16x2, ka[i]);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(a, b, acc, false);
+  }
+  return acc;
+}
+
+template <>
+__device__ inline float dot_chunk<f16_t>(const u32x4& q, const u32x4& k,
+                                         float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const uint32_t qa[4] = {q.x, q.y, q.z, q.w};
+  const uint32_t ka[4] = {k.x, k.y, k.z, k.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    h2 a = __builtin_bit_cast(h2, qa[i]);
+    h2 b = __builtin_bit_cast(h2, ka[i]);
+    acc = __builtin_amdgcn_fdot2(a, b, acc, false);
+  }
+  return acc;
+}
+
+template <>
+__device__ inline float dot_chunk<float>(const u32x4& q, const u32x4& k,
+                                         float acc) {
+  acc = fmaf(__uint_as_float(q.x), __uint_as_float(k.x), acc);
+  acc = fmaf(__uint_as_float(q.y), __uint_as_float(k.y), acc);
+  acc = fmaf(__uint_as_float(q.z), __uint_as_float(k.z), acc);
+  acc = fmaf(__uint_as_float(q.w), __uint_as_float(k.w), acc);
+  return acc;
+}
+
+template <typename T, int D>
+struct DecodeGeom {
+  static constexpr int kEPC = 16 / Elem<T>::kBytes;       // elems per chunk
+  static constexpr int kCH = D / kEPC;                     // chunks per row
+  static constexpr int kLPR = kCH < 16 ? kCH : 16;         // lanes per row
+  static constexpr int kCPL = kCH / kLPR;                  // chunks per lane
+  static constexpr int kE = kCPL * kEPC;                   // elems per lane
+  static constexpr int kRPW = 64 / kLPR;                   // rows per wave-load
+  static constexpr int kU = kE <= 8 ? 4 : 2;               // row unroll
+  static constexpr int kGCMax = kE <= 8 ? 4 : 2;           // heads per block
+  static_assert(kCH * kEPC == D, "head_dim must fill whole 16-byte chunks");
+  static_assert(kCH % kLPR == 0, "chunks must split evenly across lanes");
+};
+
+template <typename T, int D, int GC>
+__global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
+  using Geo = DecodeGeom<T, D>;
+  constexpr int EPC = Geo::kEPC, LPR = Geo::kLPR, CPL = Geo::kCPL,
+                E = Geo::kE, RPW = Geo::kRPW, U = Geo::kU;
+  extern __shared__ float smem[];
+
+  const int nw = blockDim.x >> 6;
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63;
+  const int rg = lane / LPR, li = lane % LPR;
+
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y / a.n_chunks;
+  const int chunk = blockIdx.y - kvh * a.n_chunks;
+  const int b = blockIdx.z;
+  const int h0 = kvh * a.group + chunk * a.chunk_heads;
+  const int ng = min(a.chunk_heads, a.group - chunk * a.chunk_heads);
+
+  int leff = a.kv_len;
+  if (a.seq_lens != nullptr) {
+    const int64_t sl = a.seq_lens[b];
+    leff = (int)(sl < 0 ? 0 : (sl < leff ? sl : leff));
+  }
+  const int start = split * a.split_len;
+  const int end = min(start + a.split_len, leff);
+
+  // q chunks for this lane, raw (q.k is done on the stored precision, fp32
+  // accumulate, exactly like sum(k.f32 * q.f32) in the reference).
+  u32x4 qr[GC][CPL];
+#pragma unroll
+  for (int g = 0; g < GC; ++g) {
+    const int h = h0 + min(g, ng - 1);
+    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                  (int64_t)h * a.q_sh;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int d0 = (li + j * LPR) * EPC;
+      if (a.q_vec) {
+        qr[g][j] = *reinterpret_cast<const u32x4*>(qp + d0);
+      } else {
+        union { u32x4 u; T t[EPC]; } tmp;
+#pragma unroll
+        for (int e = 0; e < EPC; ++e) tmp.t[e] = qp[(int64_t)(d0 + e) * a.q_sd];
+        qr[g][j] = tmp.u;
+      }
+    }
+  }
+
+  float m[GC], l[GC], acc[GC][E];
+#pragma unroll
+  for (int g = 0; g < GC; ++g) {
+    m[g] = kNegBig;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[g][e] = 0.f;
+  }
+
+  const T* kb = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb +
+                (int64_t)kvh * a.k_sh + li * EPC;
+  const T* vb = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb +
+                (int64_t)kvh * a.v_sh + li * EPC;
+  const uint8_t* mb =
+      a.mask != nullptr ? a.mask + (int64_t)b * a.mask_sb : nullptr;
+  const int step = U * nw * RPW;
+  const int my_off = w * RPW + rg;
+
+  for (int base = start; base < end; base += step) {
+    u32x4 kr[U][CPL], vr[U][CPL];
+    int row[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      row[u] = base + u * nw * RPW + my_off;
+      // Rows past `end` re-read the last valid row (always in bounds, never a
+      // key beyond seq_lens) and are masked out of the softmax below.
+      const int64_t rl = min(row[u], end - 1);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        kr[u][j] = load16_stream(kb + rl * a.k_sl + j * LPR * EPC);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t rl = min(row[u], end - 1);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+        vr[u][j] = load16_stream(vb + rl * a.v_sl + j * LPR * EPC);
+    }
+
+    float s[U][GC];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      bool keep = row[u] < end;
+      if (mb != nullptr && keep) keep = mb[(int64_t)row[u] * a.mask_sl] != 0;
+#pragma unroll
+      for (int g = 0; g < GC; ++g) {
+        float t = 0.f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) t = dot_chunk<T>(qr[g][j], kr[u][j], t);
+        t = group_sum<LPR>(t) * a.scale_log2;
+        s[u][g] = keep ? t : -INFINITY;
+      }
+    }
+
+    float p[U][GC];
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+      float mx = s[0][g];
+#pragma unroll
+      for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[u][g]);
+      const float mn = fmaxf(m[g], mx);
+      const float alpha = fast_exp2(m[g] - mn);
+      m[g] = mn;
+      float ls = 0.f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        p[u][g] = fast_exp2(s[u][g] - mn);
+        ls += p[u][g];
+      }
+      l[g] = l[g] * alpha + ls;
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[g][e] *= alpha;
+    }
+
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float vf[E];
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) Chunk<T>::unpack(vr[u][j], vf + j * EPC);
+#pragma unroll
+      for (int g = 0; g < GC; ++g)
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[g][e] = fmaf(p[u][g], vf[e], acc[g][e]);
+    }
+  }
+
+  // Merge the RPW row groups of this wave (butterfly over lane strides).
+#pragma unroll
+  for (int off = LPR; off < 64; off <<= 1) {
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+      const float mo = shfl_xor_f32(m[g], off);
+      const float lo = shfl_xor_f32(l[g], off);
+      const float mn = fmaxf(m[g], mo);
+      const float wa = fast_exp2(m[g] - mn), wb = fast_exp2(mo - mn);
+      l[g] = l[g] * wa + lo * wb;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float ao = shfl_xor_f32(acc[g][e], off);
+        acc[g][e] = acc[g][e] * wa + ao * wb;
+      }
+      m[g] = mn;
+    }
+  }
+
+  // Cross-wave merge through LDS: [nw][GC] m, l and [nw][GC][D] acc.
+  float* sm_m = smem;
+  float* sm_l = smem + nw * GC;
+  float* sm_acc = smem + 2 * nw * GC;
+  if (rg == 0) {
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j)
+#pragma unroll
+        for (int e = 0; e < EPC; ++e)
+          sm_acc[(w * GC + g) * D + (li + j * LPR) * EPC + e] =
+              acc[g][j * EPC + e];
+      if (li == 0) {
+        sm_m[w * GC + g] = m[g];
+        sm_l[w * GC + g] = l[g];
+      }
+    }
+  }
+  __syncthreads();
+
+  const int S = a.num_splits;
+  for (int idx = tid; idx < ng * D; idx += blockDim.x) {
+    const int g = idx / D, d = idx - g * D;
+    float M = kNegBig;
+    for (int ww = 0; ww < nw; ++ww) M = fmaxf(M, sm_m[ww * GC + g]);
+    float L = 0.f, A = 0.f;
+    for (int ww = 0; ww < nw; ++ww) {
+      const float wt = fast_exp2(sm_m[ww * GC + g] - M);
+      L += wt * sm_l[ww * GC + g];
+      A += wt * sm_acc[(ww * GC + g) * D + d];
+    }
+    const int h = h0 + g;
+    if (a.direct) {
+      float o;
+      if (L > 0.f)
+        o = A / L;
+      else
+        o = a.empty_nan ? __builtin_nanf("") : 0.f;
+      T* op = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb +
+              (int64_t)h * a.o_sh + (int64_t)d * a.o_sd;
+      *op = Elem<T>::from_f32(o);
+      if (d == 0 && a.lse != nullptr)
+        a.lse[(int64_t)b * a.n_heads + h] =
+            L > 0.f ? (M + __log2f(L)) * kLn2 : -INFINITY;
+    } else {
+      const int64_t bh = (int64_t)b * a.n_heads + h;
+      a.part_acc[(bh * S + split) * D + d] = A;
+      if (d == 0) {
+        a.part_m[bh * S + split] = M;
+        a.part_l[bh * S + split] = L;
+      }
+    }
+  }
+}
+
+struct CombineArgs {
+  const float* part_m;
+  const float* part_l;
+  const float* part_acc;
+  void* out;
+  float* lse;
+  int64_t o_sb, o_sh, o_sd;
+  int32_t n_heads, head_dim, num_splits;
+  int32_t empty_nan;
+};
+
+__device__ inline float block_reduce_max(float x, float* red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, shfl_xor_f32(x, off));
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = x;
+  __syncthreads();
+  float r = red[0];
+  for (int i = 1; i < nw; ++i) r = fmaxf(r, red[i]);
+  return r;
+}
+
+__device__ inline float block_reduce_sum(float x, float* red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += shfl_xor_f32(x, off);
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = x;
+  __syncthreads();
+  float r = 0.f;
+  for (int i = 0; i < nw; ++i) r += red[i];
+  return r;
+}
+
+// One workgroup per (batch, head): weights exp2(m_s - M) for splits with
+// l_s > 0 (src/flash_decode.py:182-192), numerator over splits in float4
+// columns, out = num/den or 0/NaN for empty rows (src/flash_decode.py:203-205).
+template <typename T>
+__global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
+  extern __shared__ float smem[];
+  __shared__ float red[8];
+  const int S = a.num_splits, D = a.head_dim;
+  const int64_t bh = blockIdx.x;
+  const int b = (int)(bh / a.n_heads), h = (int)(bh % a.n_heads);
+  const float* pm = a.part_m + bh * S;
+  const float* pl = a.part_l + bh * S;
+  const float* pacc = a.part_acc + bh * S * D;
+  float* sw = smem;                 // [S] weights
+  float* sacc = smem + S;           // [NSP][D] partial numerators
+
+  float mx = kNegBig;
+  for (int s = threadIdx.x; s < S; s += blockDim.x)
+    if (pl[s] > 0.f) mx = fmaxf(mx, pm[s]);
+  const float M = block_reduce_max(mx, red);
+
+  float den = 0.f;
+  for (int s = threadIdx.x; s < S; s += blockDim.x) {
+    const float ls = pl[s];
+    const float wt = ls > 0.f ? fast_exp2(pm[s] - M) : 0.f;
+    sw[s] = wt;
+    den += wt * ls;
+  }
+  den = block_reduce_sum(den, red);  // includes a barrier after sw[] writes
+
+  const int ncol = D >> 2;
+  const int nsp = blockDim.x / ncol;
+  const int c = threadIdx.x % ncol, sp = threadIdx.x / ncol;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (sp < nsp) {
+    for (int s = sp; s < S; s += nsp) {
+      const float wt = sw[s];
+      if (wt != 0.f) {
+        const f32x4 pv =
+            *reinterpret_cast<const f32x4*>(pacc + (int64_t)s * D + 4 * c);
+        acc += wt * pv;
+      }
+    }
+    *reinterpret_cast<f32x4*>(sacc + sp * D + 4 * c) = acc;
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    float num = 0.f;
+    for (int i = 0; i < nsp; ++i) num += sacc[i * D + d];
+    float o;
+    if (den > 0.f)
+      o = num / fmaxf(den, 1.0f);
+    else
+      o = a.empty_nan ? __builtin_nanf("") : 0.f;
+    T* op = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb +
+            (int64_t)h * a.o_sh + (int64_t)d * a.o_sd;
+    *op = Elem<T>::from_f32(o);
+  }
+  if (threadIdx.x == 0 && a.lse != nullptr)
+    a.lse[bh] = den > 0.f ? (M + __log2f(den)) * kLn2 : -INFINITY;
+}
+
+// ------------------------------------------------------------------ host
+namespace {
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
+                              dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+int elem_bytes(int32_t dtype) { return dtype == MI_DTYPE_F32 ? 4 : 2; }
+
+int gc_max(int32_t dtype, int64_t D) {
+  const int e_per_lane_chunks = (int)(D * elem_bytes(dtype) / 16);
+  const int lpr = e_per_lane_chunks < 16 ? e_per_lane_chunks : 16;
+  const int E = (e_per_lane_chunks / lpr) * (16 / elem_bytes(dtype));
+  return E <= 8 ? 4 : 2;
+}
+
+bool supported_head_dim(int32_t dtype, int64_t D) {
+  if (dtype == MI_DTYPE_F32) return D == 32 || D == 64 || D == 128 || D == 256;
+  return D == 64 || D == 128 || D == 256 || D == 32;
+}
+
+int rows_per_wave_load(int32_t dtype, int64_t D) {
+  const int ch = (int)(D * elem_bytes(dtype) / 16);
+  const int lpr = ch < 16 ? ch : 16;
+  return 64 / lpr;
+}
+
+struct Plan {
+  int n_chunks, chunk_heads, split_len, nw;
+};
+
+Plan make_plan(int32_t dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
+               int64_t D, int64_t S) {
+  Plan p;
+  const int64_t G = Hq / Hkv;
+  const int gmax = gc_max(dtype, D);
+  p.n_chunks = (int)((G + gmax - 1) / gmax);
+  p.chunk_heads = (int)((G + p.n_chunks - 1) / p.n_chunks);
+  p.split_len = (int)((L + S - 1) / S);
+  const int64_t blocks = B * Hkv * p.n_chunks * S;
+  const int cus = device_cu_count();
+  int nw = 4;
+  if (blocks < cus)
+    nw = 16;
+  else if (blocks < 2 * cus)
+    nw = 8;
+  // No more waves than the split has row-loads for.
+  const int rpw = rows_per_wave_load(dtype, D);
+  const int unroll = gc_max(dtype, D) == 4 ? 4 : 2;
+  while (nw > 1 && (int64_t)nw * rpw * unroll > p.split_len) nw >>= 1;
+  p.nw = nw;
+  return p;
+}
+
+template <typename T, int D, int GC>
+hipError_t launch_split_t(const DecodeArgs& a, const Plan& p, int64_t B,
+                          int64_t Hkv, hipStream_t stream) {
+  dim3 grid((unsigned)a.num_splits, (unsigned)(Hkv * p.n_chunks),
+            (unsigned)B);
+  dim3 block((unsigned)(p.nw * 64));
+  const size_t shmem = (size_t)p.nw * GC * (D + 2) * sizeof(float);
+  hipLaunchKernelGGL((decode_split_kernel<T, D, GC>), grid, block, shmem,
+                     stream, a);
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_split_d(const DecodeArgs& a, const Plan& p, int64_t B,
+                          int64_t Hkv, hipStream_t stream) {
+  constexpr int gmax = DecodeGeom<T, D>::kGCMax;
+  switch (p.chunk_heads) {
+    case 1: return launch_split_t<T, D, 1>(a, p, B, Hkv, stream);
+    case 2: return launch_split_t<T, D, 2>(a, p, B, Hkv, stream);
+    case 3:
+      if constexpr (gmax >= 3) return launch_split_t<T, D, 3>(a, p, B, Hkv, stream);
+      break;
+    case 4:
+      if constexpr (gmax >= 4) return launch_split_t<T, D, 4>(a, p, B, Hkv, stream);
+      break;
+    default: break;
+  }
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+hipError_t launch_split(const DecodeArgs& a, const Plan& p, int64_t B,
+                        int64_t Hkv, int64_t D, hipStream_t stream) {
+  switch (D) {
+    case 32: return launch_split_d<T, 32>(a, p, B, Hkv, stream);
+    case 64: return launch_split_d<T, 64>(a, p, B, Hkv, stream);
+    case 128: return launch_split_d<T, 128>(a, p, B, Hkv, stream);
+    case 256: return launch_split_d<T, 256>(a, p, B, Hkv, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+int32_t check_common(const void* q, const void* k, const void* v,
+                     int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
+                     int64_t D, int64_t S, int64_t k_sl, int64_t v_sl,
+                     int32_t dtype) {
+  if (q == nullptr || k == nullptr || v == nullptr) {
+    set_last_error("decode: null q/k/v pointer");
+    return MI_ERR_INVALID;
+  }
+  if (dtype != MI_DTYPE_BF16 && dtype != MI_DTYPE_F16 && dtype != MI_DTYPE_F32) {
+    set_last_error("decode: unknown dtype code %d", (int)dtype);
+    return MI_ERR_INVALID;
+  }
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || L <= 0 || D <= 0 || S <= 0) {
+    set_last_error("decode: sizes must be positive (B=%lld Hq=%lld Hkv=%lld L=%lld D=%lld splits=%lld)",
+                   (long long)B, (long long)Hq, (long long)Hkv, (long long)L,
+                   (long long)D, (long long)S);
+    return MI_ERR_INVALID;
+  }
+  if (Hq % Hkv != 0) {
+    set_last_error("decode: query heads (%lld) must be divisible by KV heads (%lld)",
+                   (long long)Hq, (long long)Hkv);
+    return MI_ERR_INVALID;
+  }
+  if (!supported_head_dim(dtype, D)) {
+    set_last_error("decode: head_dim %lld has no kernel (supported: 32, 64, 128, 256)",
+                   (long long)D);
+    return MI_ERR_UNSUPPORTED;
+  }
+  if (L > INT32_MAX / 2 || B > 65535 || Hkv * 4 > 65535 || S > INT32_MAX / 2) {
+    set_last_error("decode: shape exceeds launch limits");
+    return MI_ERR_UNSUPPORTED;
+  }
+  const int eb = elem_bytes(dtype);
+  if (((uintptr_t)k % 16) != 0 || ((uintptr_t)v % 16) != 0 ||
+      ((k_sl * eb) % 16) != 0 || ((v_sl * eb) % 16) != 0) {
+    set_last_error("decode: K/V rows must be 16-byte aligned");
+    return MI_ERR_INVALID;
+  }
+  return MI_OK;
+}
+
+DecodeArgs fill_args(const void* q, const void* k, const void* v,
+                     const uint8_t* mask, int64_t mask_sb, int64_t mask_sl,
+                     const int64_t* seq_lens, int64_t Hq, int64_t Hkv,
+                     int64_t L, int64_t S, int64_t q_sb, int64_t q_sh,
+                     int64_t q_sd, int64_t k_sb, int64_t k_sh, int64_t k_sl,
+                     int64_t v_sb, int64_t v_sh, int64_t v_sl, float sm_scale,
+                     const Plan& p, int dtype_bytes) {
+  DecodeArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.mask = mask;
+  a.mask_sb = mask_sb;
+  a.mask_sl = mask_sl;
+  a.seq_lens = seq_lens;
+  a.q_sb = q_sb; a.q_sh = q_sh; a.q_sd = q_sd;
+  a.k_sb = k_sb; a.k_sh = k_sh; a.k_sl = k_sl;
+  a.v_sb = v_sb; a.v_sh = v_sh; a.v_sl = v_sl;
+  a.n_heads = (int32_t)Hq;
+  a.group = (int32_t)(Hq / Hkv);
+  a.kv_len = (int32_t)L;
+  a.split_len = p.split_len;
+  a.num_splits = (int32_t)S;
+  a.n_chunks = p.n_chunks;
+  a.chunk_heads = p.chunk_heads;
+  a.scale_log2 = sm_scale * kLog2e;
+  const int64_t eb = dtype_bytes;
+  a.q_vec = (q_sd == 1 && ((uintptr_t)q % 16) == 0 && ((q_sb * eb) % 16) == 0 &&
+             ((q_sh * eb) % 16) == 0) ? 1 : 0;
+  return a;
+}
+
+hipError_t launch_split_any(int32_t dtype, const DecodeArgs& a, const Plan& p,
+                            int64_t B, int64_t Hkv, int64_t D,
+                            hipStream_t stream) {
+  switch (dtype) {
+    case MI_DTYPE_BF16: return launch_split<bf16_t>(a, p, B, Hkv, D, stream);
+    case MI_DTYPE_F16: return launch_split<f16_t>(a, p, B, Hkv, D, stream);
+    default: return launch_split<float>(a, p, B, Hkv, D, stream);
+  }
+}
+
+hipError_t launch_combine_any(int32_t dtype, const CombineArgs& c, int64_t B,
+                              int64_t Hq, hipStream_t stream) {
+  const int D = c.head_dim;
+  const int nsp = 256 / (D / 4);
+  const size_t shmem = ((size_t)c.num_splits + (size_t)nsp * D) * sizeof(float);
+  dim3 grid((unsigned)(B * Hq));
+  dim3 block(256);
+  switch (dtype) {
+    case MI_DTYPE_BF16:
+      hipLaunchKernelGGL(decode_combine_kernel<bf16_t>, grid, block, shmem, stream, c);
+      break;
+    case MI_DTYPE_F16:
+      hipLaunchKernelGGL(decode_combine_kernel<f16_t>, grid, block, shmem, stream, c);
+      break;
+    default:
+      hipLaunchKernelGGL(decode_combine_kernel<float>, grid, block, shmem, stream, c);
+      break;
+  }
+  return hipGetLastError();
+}
+
+constexpr int64_t kMaxSplits = 8192;
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int64_t mi_decode_default_splits(int64_t batch, int64_t n_heads,
+                                            int64_t n_kv_heads, int64_t kv_len,
+                                            int64_t head_dim) {
+  if (batch <= 0 || n_heads <= 0 || n_kv_heads <= 0 || kv_len <= 0) return 1;
+  const int64_t G = n_heads / (n_kv_heads > 0 ? n_kv_heads : 1);
+  const int gmax = gc_max(MI_DTYPE_BF16, head_dim > 0 ? head_dim : 128);
+  const int64_t chunks = (G + gmax - 1) / gmax;
+  const int64_t units = batch * n_kv_heads * (chunks > 0 ? chunks : 1);
+  const int64_t target = 2LL * device_cu_count();
+  int64_t s = (target + units - 1) / units;
+  // Keep splits at >= 256 keys so each block has real work to stream.
+  const int64_t smax = (kv_len + 255) / 256;
+  if (s > smax) s = smax;
+  if (s < 1) s = 1;
+  if (s > kMaxSplits) s = kMaxSplits;
+  return s;
+}
+
+extern "C" int32_t mi_decode_split(
+    const void* q, const void* k, const void* v, const uint8_t* mask,
+    int64_t mask_sb, int64_t mask_sl, const int64_t* seq_lens, float* part_m,
+    float* part_l, float* part_acc, int64_t batch, int64_t n_heads,
+    int64_t n_kv_heads, int64_t kv_len, int64_t head_dim, int64_t num_splits,
+    int64_t q_sb, int64_t q_sh, int64_t q_sd, int64_t k_sb, int64_t k_sh,
+    int64_t k_sl, int64_t v_sb, int64_t v_sh, int64_t v_sl, float sm_scale,
+    int32_t dtype, void* stream) {
+  int32_t st = check_common(q, k, v, batch, n_heads, n_kv_heads, kv_len,
+                            head_dim, num_splits, k_sl, v_sl, dtype);
+  if (st != MI_OK) return st;
+  if (part_m == nullptr || part_l == nullptr || part_acc == nullptr) {
+    set_last_error("decode_split: partial buffers must not be null");
+    return MI_ERR_INVALID;
+  }
+  if (num_splits > kMaxSplits) {
+    set_last_error("decode_split: num_splits %lld exceeds %lld",
+                   (long long)num_splits, (long long)kMaxSplits);
+    return MI_ERR_UNSUPPORTED;
+  }
+  Plan p = make_plan(dtype, batch, n_heads, n_kv_heads, kv_len, head_dim, num_splits);
+  DecodeArgs a = fill_args(q, k, v, mask, mask_sb, mask_sl, seq_lens, n_heads,
+                           n_kv_heads, kv_len, num_splits, q_sb, q_sh, q_sd,
+                           k_sb, k_sh, k_sl, v_sb, v_sh, v_sl, sm_scale, p,
+                           elem_bytes(dtype));
+  a.part_m = part_m;
+  a.part_l = part_l;
+  a.part_acc = part_acc;
+  a.direct = 0;
+  hipError_t e = launch_split_any(dtype, a, p, batch, n_kv_heads, head_dim,
+                                  (hipStream_t)stream);
+  if (e != hipSuccess) {
+    set_last_error("decode_split: launch failed: %s", hipGetErrorString(e));
+    return (int32_t)e;
+  }
+  return MI_OK;
+}
+
+extern "C" int32_t mi_decode_combine(const float* part_m, const float* part_l,
+                                     const float* part_acc, void* out,
+                                     float* lse, int64_t batch,
+                                     int64_t n_heads, int64_t head_dim,
+                                     int64_t num_splits, int64_t o_sb,
+                                     int64_t o_sh, int64_t o_sd,
+                                     int32_t empty_rows_nan, int32_t dtype,
+                                     void* stream) {
+  if (part_m == nullptr || part_l == nullptr || part_acc == nullptr ||
+      out == nullptr) {
+    set_last_error("decode_combine: null pointer");
+    return MI_ERR_INVALID;
+  }
+  if (batch <= 0 || n_heads <= 0 || num_splits <= 0 || head_dim <= 0) {
+    set_last_error("decode_combine: sizes must be positive");
+    return MI_ERR_INVALID;
+  }
+  if (num_splits > kMaxSplits) {
+    set_last_error("decode_combine: num_splits %lld exceeds %lld",
+                   (long long)num_splits, (long long)kMaxSplits);
+    return MI_ERR_UNSUPPORTED;
+  }
+  if (head_dim % 4 != 0 || head_dim > 1024 || (256 % (head_dim / 4)) != 0) {
+    set_last_error("decode_combine: head_dim %lld unsupported", (long long)head_dim);
+    return MI_ERR_UNSUPPORTED;
+  }
+  if (dtype != MI_DTYPE_BF16 && dtype != MI_DTYPE_F16 && dtype != MI_DTYPE_F32) {
+    set_last_error("decode_combine: unknown dtype code %d", (int)dtype);
+    return MI_ERR_INVALID;
+  }
+  CombineArgs c{};
+  c.part_m = part_m;
+  c.part_l = part_l;
+  c.part_acc = part_acc;
+  c.out = out;
+  c.lse = lse;
+  c.o_sb = o_sb; c.o_sh = o_sh; c.o_sd = o_sd;
+  c.n_heads = (int32_t)n_heads;
+  c.head_dim = (int32_t)head_dim;
+  c.num_splits = (int32_t)num_splits;
+  c.empty_nan = empty_rows_nan;
+  hipError_t e = launch_combine_any(dtype, c, batch, n_heads, (hipStream_t)stream);
+  if (e != hipSuccess) {
+    set_last_error("decode_combine: launch failed: %s", hipGetErrorString(e));
+    return (int32_t)e;
+  }
+  return MI_OK;
+}
+
+extern "C" int32_t mi_flash_decode(
+    const void* q, const void* k, const void* v, const uint8_t* mask,
+    int64_t mask_sb, int64_t mask_sl, const int64_t* seq_lens, float* part_m,
+    float* part_l, float* part_acc, void* out, float* lse, int64_t batch,
+    int64_t n_heads, int64_t n_kv_heads, int64_t kv_len, int64_t head_dim,
+    int64_t num_splits, int64_t q_sb, int64_t q_sh, int64_t q_sd, int64_t k_sb,
+    int64_t k_sh, int64_t k_sl, int64_t v_sb, int64_t v_sh, int64_t v_sl,
+    int64_t o_sb, int64_t o_sh, int64_t o_sd, float sm_scale,
+    int32_t empty_rows_nan, int32_t dtype, void* stream) {
+  if (out == nullptr) {
+    set_last_error("flash_decode: null output pointer");
+    return MI_ERR_INVALID;
+  }
+  if (num_splits != 1) {
+    int32_t st = mi_decode_split(q, k, v, mask, mask_sb, mask_sl, seq_lens,
+                                 part_m, part_l, part_acc, batch, n_heads,
+                                 n_kv_heads, kv_len, head_dim, num_splits, q_sb,
+                                 q_sh, q_sd, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl,
+                                 sm_scale, dtype, stream);
+    if (st != MI_OK) return st;
+    return mi_decode_combine(part_m, part_l, part_acc, out, lse, batch, n_heads,
+                             head_dim, num_splits, o_sb, o_sh, o_sd,
+                             empty_rows_nan, dtype, stream);
+  }
+  int32_t st = check_common(q, k, v, batch, n_heads, n_kv_heads, kv_len,
+                            head_dim, 1, k_sl, v_sl, dtype);
+  if (st != MI_OK) return st;
+  Plan p = make_plan(dtype, batch, n_heads, n_kv_heads, kv_len, head_dim, 1);
+  DecodeArgs a = fill_args(q, k, v, mask, mask_sb, mask_sl, seq_lens, n_heads,
+                           n_kv_heads, kv_len, 1, q_sb, q_sh, q_sd, k_sb, k_sh,
+                           k_sl, v_sb, v_sh, v_sl, sm_scale, p, elem_bytes(dtype));
+  a.out = out;
+  a.lse = lse;
+  a.o_sb = o_sb; a.o_sh = o_sh; a.o_sd = o_sd;
+  a.direct = 1;
+  a.empty_nan = empty_rows_nan;
+  hipError_t e = launch_split_any(dtype, a, p, batch, n_kv_heads, head_dim,
+                                  (hipStream_t)stream);
+  if (e != hipSuccess) {
+    set_last_error("flash_decode: launch failed: %s", hipGetErrorString(e));
+    return (int32_t)e;
+  }
+  return MI_OK;
+}

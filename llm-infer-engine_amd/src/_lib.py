@@ -1,0 +1,153 @@
+"""ctypes binding of libmiattn.so (the gfx950 HIP kernels behind this package).
+
+There is exactly one compute path: the HIP kernels.  If the shared library is
+missing or cannot be loaded, every op raises — there is no CPU or eager-torch
+fallback.  Build the library with ``python llm-infer-engine_amd/build_lib.py``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+import torch
+
+_PKG_ROOT = Path(__file__).resolve().parent.parent
+LIB_PATH = Path(os.environ.get("MIATTN_LIB", _PKG_ROOT / "libmiattn.so"))
+
+MI_DTYPE_BF16 = 0
+MI_DTYPE_F16 = 1
+MI_DTYPE_F32 = 2
+MI_OK = 0
+MI_ERR_INVALID = -1
+MI_ERR_UNSUPPORTED = -2
+
+_DTYPE_CODES = {
+    torch.bfloat16: MI_DTYPE_BF16,
+    torch.float16: MI_DTYPE_F16,
+    torch.float32: MI_DTYPE_F32,
+}
+
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+_f32 = ctypes.c_float
+_ptr = ctypes.c_void_p
+
+# name -> (restype, [argtypes]).  Must mirror include/miattn.h exactly.
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "mi_version": (_i32, []),
+    "mi_last_error": (ctypes.c_char_p, []),
+    "mi_decode_split": (_i32, [
+        _ptr, _ptr, _ptr,            # q k v
+        _ptr, _i64, _i64,            # mask, mask_sb, mask_sl
+        _ptr,                        # seq_lens
+        _ptr, _ptr, _ptr,            # part_m part_l part_acc
+        _i64, _i64, _i64, _i64, _i64, _i64,   # B Hq Hkv L D splits
+        _i64, _i64, _i64,            # q strides
+        _i64, _i64, _i64,            # k strides
+        _i64, _i64, _i64,            # v strides
+        _f32, _i32, _ptr,            # sm_scale dtype stream
+    ]),
+    "mi_decode_combine": (_i32, [
+        _ptr, _ptr, _ptr, _ptr, _ptr,          # part_m part_l part_acc out lse
+        _i64, _i64, _i64, _i64,                # B Hq D splits
+        _i64, _i64, _i64,                      # o strides
+        _i32, _i32, _ptr,                      # empty_nan dtype stream
+    ]),
+    "mi_flash_decode": (_i32, [
+        _ptr, _ptr, _ptr,
+        _ptr, _i64, _i64,
+        _ptr,
+        _ptr, _ptr, _ptr,
+        _ptr, _ptr,                            # out lse
+        _i64, _i64, _i64, _i64, _i64, _i64,
+        _i64, _i64, _i64,
+        _i64, _i64, _i64,
+        _i64, _i64, _i64,
+        _i64, _i64, _i64,                      # o strides
+        _f32, _i32, _i32, _ptr,                # sm_scale empty_nan dtype stream
+    ]),
+    "mi_decode_default_splits": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "mi_rope": (_i32, [
+        _ptr, _ptr, _ptr, _ptr,
+        _i64, _i64, _i64, _i64,
+        _i64, _i64, _i64, _i64,
+        _i64, _i64, _i64, _i64,
+        _i64, _i64, _i64, _i64,
+        _i32, _i32, _ptr,
+    ]),
+    "mi_rope_kv_append": (_i32, [
+        _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,    # xk xv cos sin cache_k cache_v
+        _i64, _ptr,                            # start_pos positions
+        _i64, _i64, _i64, _i64, _i64,          # B Hkv S D capacity
+        _i64, _i64, _i64, _i64,                # xk strides
+        _i64, _i64, _i64, _i64,                # xv strides
+        _i64, _i64, _i64, _i64,                # ck strides
+        _i64, _i64, _i64, _i64,                # cv strides
+        _i64, _i64, _i64, _i64,                # cos/sin strides
+        _i32, _i32, _i32, _ptr,                # cos_by_pos dtype cdtype stream
+    ]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the library; raise if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"libmiattn.so not found at {LIB_PATH}; build it with "
+                f"`python {_PKG_ROOT / 'build_lib.py'}` (the HIP kernels are the "
+                "only implementation of these ops)")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        _lib = lib
+    return _lib
+
+
+def last_error() -> str:
+    return load().mi_last_error().decode(errors="replace")
+
+
+def check(status: int, what: str) -> None:
+    """Map a C-ABI status to the Python exception the reference would raise."""
+    if status == MI_OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if status == MI_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    if status < 0:
+        raise ValueError(msg)
+    raise RuntimeError(f"{msg} (hipError {status})")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPE_CODES[dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dtype}; expected bfloat16, float16 or float32")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t: torch.Tensor) -> int:
+    """hipStream_t of torch's current stream on t's device (graph-capture aware)."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def require_device(t: torch.Tensor, what: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{what} requires CUDA tensors")

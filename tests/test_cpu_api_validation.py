@@ -1,0 +1,67 @@
+"""CPU: the Python entry points raise the reference's exceptions and messages
+for bad arguments (src/flash_decode.py:215-285, src/kv_cache.py:39-46,
+src/cuda_graph.py:10-11) before anything reaches the GPU."""
+import pytest
+import torch
+
+
+def _fd():
+    from src.flash_decode import flash_decode
+    return flash_decode
+
+
+def _t(*shape, dtype=torch.bfloat16):
+    return torch.zeros(shape, dtype=dtype)
+
+
+@pytest.mark.parametrize("q,k,v,exc,msg", [
+    (_t(2, 8, 128), _t(2, 8, 5, 128), _t(2, 8, 5, 128), ValueError, "rank-4"),
+    (_t(2, 8, 2, 128), _t(2, 8, 5, 128), _t(2, 8, 5, 128), ValueError, "query_len=1, got 2"),
+    (_t(2, 8, 1, 128), _t(2, 8, 5, 128), _t(2, 8, 6, 128), ValueError, "k and v shapes must match"),
+    (_t(2, 8, 1, 128), _t(3, 8, 5, 128), _t(3, 8, 5, 128), ValueError, "batch size and head dimension"),
+    (_t(2, 8, 1, 64), _t(2, 8, 5, 128), _t(2, 8, 5, 128), ValueError, "batch size and head dimension"),
+    (_t(2, 8, 1, 128), _t(2, 8, 0, 128), _t(2, 8, 0, 128), ValueError, "must not be empty"),
+    (_t(2, 12, 1, 128), _t(2, 8, 5, 128), _t(2, 8, 5, 128), ValueError, "divisible by KV heads"),
+    (_t(2, 8, 1, 128), _t(2, 8, 5, 128), _t(2, 8, 5, 128), ValueError, "requires CUDA tensors"),
+])
+def test_flash_decode_argument_errors(q, k, v, exc, msg):
+    with pytest.raises(exc, match=msg):
+        _fd()(q, k, v)
+
+
+def test_mask_strides_rules():
+    from src.flash_decode import _mask_strides
+    with pytest.raises(TypeError, match="torch.bool"):
+        _mask_strides(torch.zeros(10), 2, 10)
+    with pytest.raises(ValueError, match="at least one dimension"):
+        _mask_strides(torch.tensor(True), 2, 10)
+    with pytest.raises(ValueError, match="shorter"):
+        _mask_strides(torch.ones(9, dtype=torch.bool), 2, 10)
+    with pytest.raises(ValueError, match="batch dimension must be 1 or 2"):
+        _mask_strides(torch.ones(3, 10, dtype=torch.bool), 2, 10)
+    with pytest.raises(ValueError, match="except batch and KV length must be 1"):
+        _mask_strides(torch.ones(2, 2, 1, 10, dtype=torch.bool), 2, 10)
+    assert _mask_strides(torch.ones(12, dtype=torch.bool), 2, 10) == (0, 1)
+    assert _mask_strides(torch.ones(2, 12, dtype=torch.bool), 2, 10) == (12, 1)
+    assert _mask_strides(torch.ones(1, 1, 1, 12, dtype=torch.bool), 2, 10) == (0, 1)
+    assert _mask_strides(torch.ones(2, 1, 1, 12, dtype=torch.bool), 2, 10) == (12, 1)
+
+
+def test_kv_cache_position_errors():
+    from src.config import ModelArgs
+    from src.kv_cache import KVCache
+    kv = KVCache(ModelArgs(dim=64, n_layers=1, n_heads=2, n_kv_heads=1, max_seq_len=8,
+                           device="cpu"), dtype=torch.bfloat16)
+    assert kv.k.shape == (1, 1, 1, 8, 32)
+    with pytest.raises(ValueError, match="1D tensor"):
+        kv.update_positions(0, torch.zeros(1, 1, dtype=torch.long), _t(1, 1, 1, 32), _t(1, 1, 1, 32))
+    with pytest.raises(ValueError, match="length mismatch"):
+        kv.update_positions(0, torch.zeros(2, dtype=torch.long), _t(1, 1, 1, 32), _t(1, 1, 1, 32))
+
+
+def test_model_args_defaults_are_llama_3_2_1b():
+    from src.config import ModelArgs
+    a = ModelArgs()
+    assert (a.dim, a.n_layers, a.n_heads, a.n_kv_heads, a.vocab_size, a.hidden_dim) == \
+        (2048, 16, 32, 8, 128256, 8192)
+    assert (a.norm_eps, a.max_batch_size, a.max_seq_len, a.rope_theta) == (1e-5, 1, 4096, 500000.0)

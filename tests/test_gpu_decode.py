@@ -1,0 +1,174 @@
+"""GPU parity: split-KV flash decode (HIP) vs the CPU oracle.
+
+Tolerances (north_star): bf16 outputs within 2e-2 max-abs of the fp32 CPU
+oracle on the same bf16 inputs, fp32 LSE within 1e-3.  fp16/fp32 outputs use
+tighter bounds (5e-3 / 1e-4).
+"""
+import pytest
+import torch
+
+from helpers import max_abs, randn
+from oracle import attention as ora
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.bfloat16: 2e-2, torch.float16: 5e-3, torch.float32: 1e-4}
+LSE_TOL = 1e-3
+
+
+def _fd():
+    from src.flash_decode import flash_decode
+    return flash_decode
+
+
+def _inputs(B, Hq, Hkv, L, D, dtype, dev, seed=0, T=None):
+    T = T or L
+    q = randn((B, Hq, 1, D), seed, dtype, dev)
+    k = randn((B, Hkv, T, D), seed + 1, dtype, dev)[:, :, :L]
+    v = randn((B, Hkv, T, D), seed + 2, dtype, dev)[:, :, :L]
+    return q, k, v
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Hq,Hkv", [(24, 8), (32, 8), (8, 8), (16, 2)])
+def test_decode_matches_oracle(dev, dtype, D, Hq, Hkv):
+    B, L = 3, 777
+    q, k, v = _inputs(B, Hq, Hkv, L, D, dtype, dev)
+    out, lse = _fd()(q, k, v, return_lse=True)
+    ref, ref_lse = ora.decode(q, k, v)
+    assert out.dtype == dtype and out.shape == q.shape
+    assert max_abs(out, ref) < TOL[dtype]
+    assert max_abs(lse, ref_lse) < LSE_TOL
+
+
+@pytest.mark.parametrize("num_splits", [1, 2, 7, 16, 64, 200])
+def test_split_count_invariance(dev, num_splits):
+    q, k, v = _inputs(2, 24, 8, 3001, 128, torch.bfloat16, dev, seed=5)
+    out, lse = _fd()(q, k, v, num_splits=num_splits, return_lse=True)
+    ref, ref_lse = ora.decode(q, k, v)
+    assert max_abs(out, ref) < 2e-2
+    assert max_abs(lse, ref_lse) < LSE_TOL
+
+
+@pytest.mark.parametrize("D", [32, 256])
+def test_decode_other_head_dims(dev, D):
+    q, k, v = _inputs(2, 6, 2, 515, D, torch.bfloat16, dev, seed=9)
+    out, lse = _fd()(q, k, v, return_lse=True)
+    ref, ref_lse = ora.decode(q, k, v)
+    assert max_abs(out, ref) < 2e-2
+    assert max_abs(lse, ref_lse) < LSE_TOL
+
+
+@pytest.mark.parametrize("shape", ["1d", "2d", "4d", "4d_b1"])
+def test_mask_shapes(dev, shape):
+    B, Hq, Hkv, L, D = 4, 24, 8, 1200, 128
+    q, k, v = _inputs(B, Hq, Hkv, L, D, torch.bfloat16, dev, seed=11)
+    g = torch.Generator("cpu").manual_seed(3)
+    Lp = L + 37  # masks may be longer than the KV sequence
+    if shape == "1d":
+        mask = torch.rand(Lp, generator=g) < 0.6
+    elif shape == "2d":
+        mask = torch.rand(B, Lp, generator=g) < 0.6
+    elif shape == "4d":
+        mask = torch.rand(B, 1, 1, Lp, generator=g) < 0.6
+    else:
+        mask = torch.rand(1, 1, 1, Lp, generator=g) < 0.6
+    mask = mask.to(dev)
+    out, lse = _fd()(q, k, v, mask=mask, return_lse=True)
+    ref, ref_lse = ora.decode(q, k, v, mask=mask)
+    assert max_abs(out, ref) < 2e-2
+    assert max_abs(lse, ref_lse) < LSE_TOL
+
+
+def test_all_ones_mask_equals_none(dev):
+    q, k, v = _inputs(2, 24, 8, 999, 128, torch.bfloat16, dev, seed=2)
+    mask = torch.ones(2, 999, dtype=torch.bool, device=dev)
+    a = _fd()(q, k, v, mask=mask, num_splits=4)
+    b = _fd()(q, k, v, num_splits=4)
+    assert torch.equal(a, b)
+
+
+def test_fully_masked_row_is_zero_and_legacy_nan(dev):
+    from src.decode_attn import decode_attention
+    B, L = 3, 500
+    q, k, v = _inputs(B, 24, 8, L, 128, torch.bfloat16, dev, seed=4)
+    mask = torch.ones(B, 1, 1, L, dtype=torch.bool)
+    mask[1] = False
+    mask = mask.to(dev)
+    out, lse = _fd()(q, k, v, mask=mask, return_lse=True)
+    ref, ref_lse = ora.decode(q, k, v, mask=mask)
+    assert torch.all(out[1] == 0)
+    assert torch.all(torch.isneginf(lse[1]))
+    assert max_abs(out, ref) < 2e-2
+    legacy = decode_attention(q, k, v, mask=mask)
+    assert torch.all(torch.isnan(legacy[1]))
+    assert max_abs(legacy[0], ref[0]) < 2e-2 and max_abs(legacy[2], ref[2]) < 2e-2
+
+
+def test_seq_lens_never_reads_beyond_length(dev):
+    """Slots >= seq_lens[b] hold NaN; a single read of one would poison out."""
+    B, Hq, Hkv, T, D = 5, 24, 8, 2048, 128
+    q, k, v = _inputs(B, Hq, Hkv, T, D, torch.bfloat16, dev, seed=7)
+    lens = torch.tensor([1, 17, 1024, 1500, 2048], dtype=torch.int64)
+    k = k.clone()
+    v = v.clone()
+    for b in range(B):
+        k[b, :, lens[b]:] = float("nan")
+        v[b, :, lens[b]:] = float("nan")
+    for splits in (1, 5, 32):
+        out, lse = _fd()(q, k, v, seq_lens=lens.to(dev), num_splits=splits, return_lse=True)
+        assert not torch.isnan(out).any()
+        ref, ref_lse = ora.decode(q, k, v, seq_lens=lens)
+        assert max_abs(out, ref) < 2e-2
+        assert max_abs(lse, ref_lse) < LSE_TOL
+
+
+def test_length_one_returns_v0(dev):
+    q, k, v = _inputs(2, 24, 8, 1, 128, torch.bfloat16, dev, seed=8)
+    out = _fd()(q, k, v)
+    G = 3
+    expect = v[:, :, 0].repeat_interleave(G, dim=1)
+    assert torch.equal(out[:, :, 0], expect)
+
+
+def test_strided_q_and_cache_views(dev):
+    """q as a transposed [B,S,H,D] view; k/v as layer views of a bigger cache."""
+    B, Hq, Hkv, T, L, D = 2, 24, 8, 4096, 1500, 128
+    xq = randn((B, 1, Hq, D), 1, torch.bfloat16, dev)
+    q = xq.transpose(1, 2)
+    cache = randn((3, B, Hkv, T, D), 2, torch.bfloat16, dev)
+    cache_v = randn((3, B, Hkv, T, D), 3, torch.bfloat16, dev)
+    k, v = cache[1, :, :, :L], cache_v[1, :, :, :L]
+    out = _fd()(q, k, v)
+    ref, _ = ora.decode(q, k, v)
+    assert out.stride() == q.stride()
+    assert max_abs(out, ref) < 2e-2
+
+
+def test_config3_full_size(dev):
+    """B16, 24/8, D128, T=8192, L_b ~ randint(1024, 8193)."""
+    g = torch.Generator("cpu").manual_seed(0)
+    lens = torch.randint(1024, 8193, (16,), generator=g)
+    assert int(lens.sum()) == 96634
+    q = (torch.randn((16, 24, 1, 128), generator=g)).to(torch.bfloat16)
+    kc = (torch.randn((16, 8, 8192, 128), generator=g)).to(torch.bfloat16)
+    vc = (torch.randn((16, 8, 8192, 128), generator=g)).to(torch.bfloat16)
+    mask = torch.arange(8192)[None, :] < lens[:, None]
+    qd, kd, vd = q.to(dev), kc.to(dev), vc.to(dev)
+    ref, ref_lse = ora.decode(q, kc, vc, seq_lens=lens)
+    out_m, lse_m = _fd()(qd, kd, vd, mask=mask.to(dev), return_lse=True)
+    out_s, lse_s = _fd()(qd, kd, vd, seq_lens=lens.to(dev), return_lse=True)
+    for o, l in ((out_m, lse_m), (out_s, lse_s)):
+        assert max_abs(o, ref) < 2e-2
+        assert max_abs(l, ref_lse) < LSE_TOL
+
+
+@pytest.mark.parametrize("num_splits", [16, 32, 64, 128])
+def test_config4_long_context(dev, num_splits):
+    """B1, L=131072, 24/8, D128 (beyond the reference's cap)."""
+    q, k, v = _inputs(1, 24, 8, 131072, 128, torch.bfloat16, dev, seed=0)
+    out, lse = _fd()(q, k, v, num_splits=num_splits, return_lse=True)
+    ref, ref_lse = ora.decode(q, k, v)
+    assert max_abs(out, ref) < 2e-2
+    assert max_abs(lse, ref_lse) < LSE_TOL
