@@ -159,6 +159,26 @@ int32_t mi_rope_kv_append(const void* xk, const void* xv, const void* cos,
                           int64_t s_sd, int32_t cos_by_position, int32_t dtype,
                           int32_t cdtype, void* stream);
 
+/*
+ * Causal GQA prefill attention with optional fp32 LSE output.
+ * q [batch, n_heads, seq_len, head_dim], k/v [batch, n_kv_heads, kv_len,
+ * head_dim] (kv_len >= seq_len; only the first seq_len keys are used and
+ * query row i attends keys 0..i), out like q, lse [batch, n_heads, seq_len]
+ * fp32 (natural log of the scaled scores) or NULL.  Unit head-dim stride,
+ * 16-byte aligned rows.  head_dim 64 or 128; bf16/fp16 run on MFMA, fp32 on
+ * VALU.  Query head h reads kv head h / (n_heads / n_kv_heads).
+ * Replaces flash_attention_kernel + flash_attention
+ *   src/flash_attn.py:5-83, src/flash_attn.py:85-111.
+ */
+int32_t mi_attn_prefill(const void* q, const void* k, const void* v, void* out,
+                        float* lse, int64_t batch, int64_t n_heads,
+                        int64_t n_kv_heads, int64_t seq_len, int64_t kv_len,
+                        int64_t head_dim, int64_t q_sb, int64_t q_sh,
+                        int64_t q_ss, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                        int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb,
+                        int64_t o_sh, int64_t o_ss, float sm_scale,
+                        int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

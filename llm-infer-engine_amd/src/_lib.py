@@ -69,6 +69,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _f32, _i32, _i32, _ptr,                # sm_scale empty_nan dtype stream
     ]),
     "mi_decode_default_splits": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "mi_attn_prefill": (_i32, [
+        _ptr, _ptr, _ptr, _ptr, _ptr,          # q k v out lse
+        _i64, _i64, _i64, _i64, _i64, _i64,    # B Hq Hkv S L D
+        _i64, _i64, _i64,                      # q strides (b, h, s)
+        _i64, _i64, _i64,                      # k strides
+        _i64, _i64, _i64,                      # v strides
+        _i64, _i64, _i64,                      # out strides
+        _f32, _i32, _ptr,                      # sm_scale dtype stream
+    ]),
     "mi_rope": (_i32, [
         _ptr, _ptr, _ptr, _ptr,
         _i64, _i64, _i64, _i64,
