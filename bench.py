@@ -1,0 +1,270 @@
+"""Benchmark of the MI355X attention hot path (one JSON line on stdout).
+
+Headline (`value`): BASELINE config 2 — causal GQA prefill, bf16, B4 S2048
+32/8 heads D64, fp32 LSE output, in TFLOP/s of algorithmic work
+(4*B*Hq*S^2*D/2 = 68.72 GFLOP per step).  The same line carries, under
+`extra`, the HBM-bound decode configs (3: B16 24/8 D128 T8192 ragged lengths;
+4: B1 L=131072, split sweep) in GB/s, each with its own roofline, and the CPU
+baseline (the fp32 oracle on the host cores, on a bounded sample).
+
+A step is one flash_attention call on resident inputs.  Timing: W untimed
+warm-up steps, then K steps between torch.cuda.synchronize() calls, with HIP
+events (torch's current stream — the stream the kernels are launched on).
+Decode steps are replayed from captured hipGraphs (one per rotating buffer set,
+so the 256 MB MALL cannot serve repeated reads).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT / "llm-infer-engine_amd"), str(ROOT)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2516.6      # MI355X dense bf16 MFMA, TFLOP/s
+
+
+def _cpu_name() -> str:
+    try:
+        for ln in open("/proc/cpuinfo"):
+            if ln.startswith("model name"):
+                return ln.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def _traffic(name: str):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    f = ROOT / "profiles" / f"{name}_traffic.json"
+    if f.exists():
+        try:
+            return json.loads(f.read_text()).get("bytes_per_launch")
+        except (ValueError, OSError):
+            return None
+    return None
+
+
+def bench_prefill(torch, steps: int, warmup: int) -> dict:
+    from src.flash_attn import flash_attention
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, S, D = 4, 32, 8, 2048, 64
+    g = torch.Generator("cpu").manual_seed(0)
+    # config 2: Q/K/V ~ N(0,1), Q scaled by 1/sqrt(64) (softmax scale folded in)
+    q = (torch.randn((B, Hq, S, D), generator=g) / 8.0).to(torch.bfloat16).to(dev)
+    k = torch.randn((B, Hkv, S, D), generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn((B, Hkv, S, D), generator=g).to(torch.bfloat16).to(dev)
+    flops = 4.0 * B * Hq * S * S * D / 2
+    step = lambda: flash_attention(q, k, v, sm_scale=1.0, return_lse=True)  # noqa: E731
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    # per-launch duration: events around single launches (GPU kept busy by a
+    # queued launch in front so the start event is not taken while idle)
+    durs = []
+    for _ in range(max(3, min(steps, 10))):
+        step()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        step()
+        b.record()
+        torch.cuda.synchronize()
+        durs.append(a.elapsed_time(b))
+    durs.sort()
+    kern_ms = durs[len(durs) // 2]
+    achieved = flops / (kern_ms * 1e-3) / 1e12
+    return {
+        "ms_per_step": ms,
+        "value": flops / (ms * 1e-3) / 1e12,
+        "kernel_ms": kern_ms,
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                     "traffic": _traffic("prefill_config2")},
+        "flops": flops,
+    }
+
+
+def _graph_decode(torch, fn, n_sets):
+    graphs = []
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(n_sets):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for i in range(n_sets):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            fn(i)
+        graphs.append(gr)
+    return graphs
+
+
+def _time_graphs(torch, graphs, steps, warmup):
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps
+
+
+def bench_decode_cfg3(torch, steps: int, warmup: int) -> dict:
+    from src.flash_decode import flash_decode
+    dev = torch.device("cuda:0")
+    g = torch.Generator("cpu").manual_seed(0)
+    lens = torch.randint(1024, 8193, (16,), generator=g)
+    n_sets = 3  # 3 x 537 MB of K/V: well past the 256 MB MALL
+    qs, ks, vs = [], [], []
+    for _ in range(n_sets):
+        qs.append(torch.randn((16, 24, 1, 128), generator=g).to(torch.bfloat16).to(dev))
+        ks.append(torch.randn((16, 8, 8192, 128), generator=g).to(torch.bfloat16).to(dev))
+        vs.append(torch.randn((16, 8, 8192, 128), generator=g).to(torch.bfloat16).to(dev))
+    sl = lens.to(dev)
+    nbytes = int(lens.sum()) * 8 * 128 * 2 * 2 + 2 * 16 * 24 * 128 * 2
+    graphs = _graph_decode(torch, lambda i: flash_decode(qs[i], ks[i], vs[i], seq_lens=sl), n_sets)
+    ms = _time_graphs(torch, graphs, max(steps, 20), warmup)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out = {
+        "config": "3: decode B16 24/8 D128 T8192 L~U[1024,8192] (sum 96634), seq_lens, hipGraph",
+        "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": ms, "bytes": nbytes,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": _traffic("decode_config3")},
+    }
+    del graphs, ks, vs
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_decode_cfg4(torch, steps: int, warmup: int) -> dict:
+    from src.flash_decode import flash_decode
+    dev = torch.device("cuda:0")
+    g = torch.Generator("cpu").manual_seed(0)
+    n_sets = 2  # 2 x 537 MB
+    qs = [torch.randn((1, 24, 1, 128), generator=g).to(torch.bfloat16).to(dev) for _ in range(n_sets)]
+    ks = [torch.randn((1, 8, 131072, 128), generator=g).to(torch.bfloat16).to(dev) for _ in range(n_sets)]
+    vs = [torch.randn((1, 8, 131072, 128), generator=g).to(torch.bfloat16).to(dev) for _ in range(n_sets)]
+    nbytes = 131072 * 8 * 128 * 2 * 2 + 2 * 24 * 128 * 2
+    sweep = {}
+    for splits in (16, 32, 64, 128):
+        graphs = _graph_decode(
+            torch, lambda i, s=splits: flash_decode(qs[i], ks[i], vs[i], num_splits=s), n_sets)
+        ms = _time_graphs(torch, graphs, max(steps, 20), warmup)
+        sweep[str(splits)] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        del graphs
+    best = max(sweep.values())
+    out = {"config": "4: decode B1 L131072 24/8 D128, splits sweep (combine included)",
+           "unit": "GB/s", "by_splits": sweep, "value": best,
+           "roofline": {"bound": "hbm", "achieved": best, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(best / HBM_PEAK_GBS, 4), "traffic": None}}
+    del ks, vs
+    torch.cuda.empty_cache()
+    return out
+
+
+def cpu_baseline(torch) -> dict:
+    """The fp32 CPU oracle on batch 0 of config 2 (1/4 of a step), on rank 0."""
+    from oracle import attention as ora
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    g = torch.Generator("cpu").manual_seed(0)
+    q = (torch.randn((4, 32, 2048, 64), generator=g) / 8.0).to(torch.bfloat16)[:1]
+    k = torch.randn((4, 8, 2048, 64), generator=g).to(torch.bfloat16)[:1]
+    v = torch.randn((4, 8, 2048, 64), generator=g).to(torch.bfloat16)[:1]
+    flops = 4.0 * 1 * 32 * 2048 * 2048 * 64 / 2
+    ora.prefill(q, k, v, sm_scale=1.0)
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        ora.prefill(q, k, v, sm_scale=1.0)
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    t = ts[1]
+    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle.prefill (torch fp32, CPU) on batch 0 of config 2 = 1/4 step "
+                      f"({flops/1e9:.2f} GFLOP), median of 3 after 1 warm-up: {t:.2f} s; "
+                      f"host {_cpu_name()}"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "decode"], default=None,
+                    help="run one leg only (profiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(--gpus {args.gpus} requested)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(1)
+
+    extra = {}
+    pre = None
+    if args.only in (None, "prefill"):
+        pre = bench_prefill(torch, args.steps, args.warmup)
+    if args.only in (None, "decode"):
+        extra["decode_config3"] = bench_decode_cfg3(torch, args.steps, args.warmup)
+        extra["decode_config4"] = bench_decode_cfg4(torch, args.steps, args.warmup)
+    cpu = None
+    if not args.no_cpu_baseline and args.only is None:
+        cpu = cpu_baseline(torch)
+    line = {
+        "metric": "flash-decode HBM GB/s (% of peak) + prefill attn TFLOP/s, 1 MI355X",
+        "value": round(pre["value"], 1) if pre else None,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["ms_per_step"], 4) if pre else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) inputs (torch.Generator seed 0), no checkpoint",
+        "config": {"workload": "config 2: causal GQA prefill B4 S2048 Hq32 Hkv8 D64, "
+                               "bf16 in/out, fp32 accumulate + fp32 LSE",
+                   "batch": 4, "seq_len": 2048, "n_heads": 32, "n_kv_heads": 8,
+                   "head_dim": 64, "flops_per_step": pre["flops"] if pre else None},
+        "roofline": pre["roofline"] if pre else None,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -123,11 +123,12 @@ int64_t mi_decode_default_splits(int64_t batch, int64_t n_heads,
 /*
  * Rotate-half RoPE of x [batch, n_heads, seq_len, head_dim] into out (any
  * strides).  Row s uses cos/sin row s of the [seq_len, head_dim/2] tables
- * (the caller slices the table at start_pos).  cdtype is the table dtype.
+ * (the caller slices the table at start_pos), or row positions[s] when
+ * positions (device int64 [seq_len]) is not NULL.  cdtype is the table dtype.
  * Replaces rope_kernel + apply_rotary  src/rope.py:48-91, src/rope.py:94-119.
  */
 int32_t mi_rope(const void* x, void* out, const void* cos, const void* sin,
-                int64_t batch, int64_t n_heads, int64_t seq_len,
+                const int64_t* positions, int64_t batch, int64_t n_heads, int64_t seq_len,
                 int64_t head_dim, int64_t x_sb, int64_t x_sh, int64_t x_ss,
                 int64_t x_sd, int64_t o_sb, int64_t o_sh, int64_t o_ss,
                 int64_t o_sd, int64_t c_ss, int64_t c_sd, int64_t s_ss,
@@ -178,6 +179,39 @@ int32_t mi_attn_prefill(const void* q, const void* k, const void* v, void* out,
                         int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb,
                         int64_t o_sh, int64_t o_ss, float sm_scale,
                         int32_t dtype, void* stream);
+
+/*
+ * RMSNorm over the last dim: y[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w,
+ * fp32 internally, y in x's dtype (wdtype = weight dtype).  rows x n with row
+ * strides x_rs / y_rs.
+ * Replaces rms_norm_fwd_kernel + rmsnorm_triton  src/rms_norm.py:18-77.
+ */
+int32_t mi_rmsnorm(const void* x, const void* w, void* y, int64_t rows,
+                   int64_t n, int64_t x_rs, int64_t y_rs, float eps,
+                   int32_t dtype, int32_t wdtype, void* stream);
+
+/*
+ * Symmetric per-output-channel int8 quantisation of w [n_rows, k] (dtype):
+ * scales[n] = dtype(max(max|w[n,:]|, 1e-12) / 127), q = clamp(rne(w / s),
+ * -128, 127), every step IEEE-rounded (bit-exact with the reference recipe).
+ * Replaces quantize_weight_symmetric_per_channel  src/quant_utils.py:7-36.
+ */
+int32_t mi_quantize_int8(const void* w, int8_t* q, void* scales,
+                         int64_t n_rows, int64_t k, int64_t w_rs, int64_t q_rs,
+                         int32_t dtype, void* stream);
+
+/*
+ * W8A16 GEMV, 1 <= m <= 16: y[m, n] = (sum_k x[m,k] * w[n,k]) * scales[n],
+ * fp32 accumulate on MFMA, y in x's dtype (bf16/fp16).  w int8 [n, k] with
+ * 16-byte aligned rows, k % 16 == 0.  sdtype = scales dtype.
+ * Replaces w8a16_gemv_kernel + w8a16_gemv_launch
+ *   src/quant_linear.py:7-63, src/quant_linear.py:66-120.
+ */
+int32_t mi_w8a16_gemv(const void* x, const int8_t* w, const void* scales,
+                      void* y, int64_t m, int64_t n, int64_t k, int64_t x_sm,
+                      int64_t x_sk, int64_t w_sn, int64_t s_sn, int64_t y_sm,
+                      int64_t y_sn, int32_t dtype, int32_t sdtype,
+                      void* stream);
 
 #ifdef __cplusplus
 }

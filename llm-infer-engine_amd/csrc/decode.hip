@@ -326,77 +326,71 @@ struct CombineArgs {
   int32_t empty_nan;
 };
 
-__device__ inline float block_reduce_max(float x, float* red) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x = fmaxf(x, shfl_xor_f32(x, off));
-  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = x;
-  __syncthreads();
-  float r = red[0];
-  for (int i = 1; i < nw; ++i) r = fmaxf(r, red[i]);
-  return r;
-}
-
-__device__ inline float block_reduce_sum(float x, float* red) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += shfl_xor_f32(x, off);
-  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[w] = x;
-  __syncthreads();
-  float r = 0.f;
-  for (int i = 0; i < nw; ++i) r += red[i];
-  return r;
-}
-
 // One workgroup per (batch, head): weights exp2(m_s - M) for splits with
 // l_s > 0 (src/flash_decode.py:182-192), numerator over splits in float4
 // columns, out = num/den or 0/NaN for empty rows (src/flash_decode.py:203-205).
+// Latency-bound (a few KB per row): every thread issues all of its partial
+// loads before it reduces, so a call costs ~2 L2 round trips, not one per split.
 template <typename T>
 __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
+  constexpr int kUnroll = 8;
   extern __shared__ float smem[];
-  __shared__ float red[8];
+  __shared__ float red[2][4];
   const int S = a.num_splits, D = a.head_dim;
   const int64_t bh = blockIdx.x;
   const int b = (int)(bh / a.n_heads), h = (int)(bh % a.n_heads);
   const float* pm = a.part_m + bh * S;
   const float* pl = a.part_l + bh * S;
   const float* pacc = a.part_acc + bh * S * D;
-  float* sw = smem;                 // [S] weights
-  float* sacc = smem + S;           // [NSP][D] partial numerators
+  float* sw = smem;        // [S] weights
+  float* sacc = smem + S;  // [NSP][D] partial numerators
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 
+  // max over non-empty splits
   float mx = kNegBig;
-  for (int s = threadIdx.x; s < S; s += blockDim.x)
+  for (int s = tid; s < S; s += 256)
     if (pl[s] > 0.f) mx = fmaxf(mx, pm[s]);
-  const float M = block_reduce_max(mx, red);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, shfl_xor_f32(mx, off));
+  if (lane == 0) red[0][w] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
 
   float den = 0.f;
-  for (int s = threadIdx.x; s < S; s += blockDim.x) {
+  for (int s = tid; s < S; s += 256) {
     const float ls = pl[s];
     const float wt = ls > 0.f ? fast_exp2(pm[s] - M) : 0.f;
     sw[s] = wt;
     den += wt * ls;
   }
-  den = block_reduce_sum(den, red);  // includes a barrier after sw[] writes
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) den += shfl_xor_f32(den, off);
+  if (lane == 0) red[1][w] = den;
+  __syncthreads();  // also publishes sw[]
+  den = red[1][0] + red[1][1] + red[1][2] + red[1][3];
 
   const int ncol = D >> 2;
-  const int nsp = blockDim.x / ncol;
-  const int c = threadIdx.x % ncol, sp = threadIdx.x / ncol;
+  const int nsp = 256 / ncol;
+  const int c = tid % ncol, sp = tid / ncol;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  if (sp < nsp) {
-    for (int s = sp; s < S; s += nsp) {
-      const float wt = sw[s];
-      if (wt != 0.f) {
-        const f32x4 pv =
-            *reinterpret_cast<const f32x4*>(pacc + (int64_t)s * D + 4 * c);
-        acc += wt * pv;
-      }
+  for (int s0 = sp; s0 < S; s0 += nsp * kUnroll) {
+    f32x4 pv[kUnroll];
+    float wt[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int s = s0 + u * nsp;
+      const bool ok = s < S;
+      wt[u] = ok ? sw[s] : 0.f;
+      pv[u] = ok ? *reinterpret_cast<const f32x4*>(pacc + (int64_t)s * D + 4 * c)
+                 : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    *reinterpret_cast<f32x4*>(sacc + sp * D + 4 * c) = acc;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (wt[u] != 0.f) acc += wt[u] * pv[u];
   }
+  *reinterpret_cast<f32x4*>(sacc + sp * D + 4 * c) = acc;
   __syncthreads();
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+  for (int d = tid; d < D; d += 256) {
     float num = 0.f;
     for (int i = 0; i < nsp; ++i) num += sacc[i * D + d];
     float o;
@@ -408,7 +402,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
             (int64_t)h * a.o_sh + (int64_t)d * a.o_sd;
     *op = Elem<T>::from_f32(o);
   }
-  if (threadIdx.x == 0 && a.lse != nullptr)
+  if (tid == 0 && a.lse != nullptr)
     a.lse[bh] = den > 0.f ? (M + __log2f(den)) * kLn2 : -INFINITY;
 }
 

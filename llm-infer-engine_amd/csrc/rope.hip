@@ -21,6 +21,7 @@ struct RopeArgs {
   void* out;
   const void* cos;
   const void* sin;
+  const int64_t* positions;  // null: table row s; else row positions[s]
   int64_t x_sb, x_sh, x_ss, x_sd;
   int64_t o_sb, o_sh, o_ss, o_sd;
   int64_t c_ss, c_sd, s_ss, s_sd;
@@ -52,8 +53,9 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     const int b = (int)(r / a.H);
     const T* xp = reinterpret_cast<const T*>(a.x) + b * a.x_sb + h * a.x_sh + s * a.x_ss;
     T* op = reinterpret_cast<T*>(a.out) + b * a.o_sb + h * a.o_sh + s * a.o_ss;
-    const CT* cp = reinterpret_cast<const CT*>(a.cos) + s * a.c_ss + i * a.c_sd;
-    const CT* sp = reinterpret_cast<const CT*>(a.sin) + s * a.s_ss + i * a.s_sd;
+    const int64_t crow = a.positions != nullptr ? a.positions[s] : s;
+    const CT* cp = reinterpret_cast<const CT*>(a.cos) + crow * a.c_ss + i * a.c_sd;
+    const CT* sp = reinterpret_cast<const CT*>(a.sin) + crow * a.s_ss + i * a.s_sd;
     const float x1 = Elem<T>::to_f32(xp[i * a.x_sd]);
     const float x2 = Elem<T>::to_f32(xp[(i + a.half) * a.x_sd]);
     T y1, y2;
@@ -159,7 +161,8 @@ using namespace mi;
   } while (0)
 
 extern "C" int32_t mi_rope(const void* x, void* out, const void* cos,
-                           const void* sin, int64_t batch, int64_t n_heads,
+                           const void* sin, const int64_t* positions,
+                           int64_t batch, int64_t n_heads,
                            int64_t seq_len, int64_t head_dim, int64_t x_sb,
                            int64_t x_sh, int64_t x_ss, int64_t x_sd,
                            int64_t o_sb, int64_t o_sh, int64_t o_ss,
@@ -181,7 +184,7 @@ extern "C" int32_t mi_rope(const void* x, void* out, const void* cos,
   const int64_t total = batch * n_heads * seq_len * (head_dim / 2);
   if (total == 0) return MI_OK;
   RopeArgs a{};
-  a.x = x; a.out = out; a.cos = cos; a.sin = sin;
+  a.x = x; a.out = out; a.cos = cos; a.sin = sin; a.positions = positions;
   a.x_sb = x_sb; a.x_sh = x_sh; a.x_ss = x_ss; a.x_sd = x_sd;
   a.o_sb = o_sb; a.o_sh = o_sh; a.o_ss = o_ss; a.o_sd = o_sd;
   a.c_ss = c_ss; a.c_sd = c_sd; a.s_ss = s_ss; a.s_sd = s_sd;

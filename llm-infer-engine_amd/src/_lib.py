@@ -79,7 +79,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _f32, _i32, _ptr,                      # sm_scale dtype stream
     ]),
     "mi_rope": (_i32, [
-        _ptr, _ptr, _ptr, _ptr,
+        _ptr, _ptr, _ptr, _ptr, _ptr,          # x out cos sin positions
         _i64, _i64, _i64, _i64,
         _i64, _i64, _i64, _i64,
         _i64, _i64, _i64, _i64,
@@ -96,6 +96,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i64, _i64, _i64, _i64,                # cv strides
         _i64, _i64, _i64, _i64,                # cos/sin strides
         _i32, _i32, _i32, _ptr,                # cos_by_pos dtype cdtype stream
+    ]),
+    "mi_rmsnorm": (_i32, [
+        _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _f32, _i32, _i32, _ptr,
+    ]),
+    "mi_quantize_int8": (_i32, [
+        _ptr, _ptr, _ptr, _i64, _i64, _i64, _i64, _i32, _ptr,
+    ]),
+    "mi_w8a16_gemv": (_i32, [
+        _ptr, _ptr, _ptr, _ptr,                # x w scales y
+        _i64, _i64, _i64,                      # M N K
+        _i64, _i64, _i64, _i64, _i64, _i64,    # x_sm x_sk w_sn s_sn y_sm y_sn
+        _i32, _i32, _ptr,                      # dtype sdtype stream
     ]),
 }
 

@@ -1,0 +1,86 @@
+"""hipGraph-captured decode step (interface of src/cuda_graph.py).
+
+``CUDAGraphDecodeRunner(model, model_args, kv_cache, device)`` keeps the
+reference's name and ``decode(token_id, current_pos) -> logits`` contract
+(src/cuda_graph.py:8-70); on ROCm torch.cuda.CUDAGraph is a hipGraph.  What the
+MI355X version changes:
+  * batch support: one token per sequence, ``batch_size`` rows (the reference
+    captures batch 1 only); all rows share the decode position, as the
+    reference's scatter path does (src/rope.py:216);
+  * nothing is copied from the host per step except the token ids: position
+    and per-row visible lengths are written with device fills, and RoPE rows
+    are gathered on the device from the model's resident cos/sin table (the
+    reference copies a freqs row from the CPU table every step, :64);
+  * attention reads exactly pos+1 keys per row through ``seq_lens`` instead of
+    scanning all max_seq_len slots behind a rewritten bool mask (:65-66).
+All launches inside the graph are the HIP kernels of libmiattn.so plus the
+library GEMMs/elementwise ops of the model.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from .config import ModelArgs
+from .kv_cache import KVCache
+
+
+class CUDAGraphDecodeRunner:
+    def __init__(self, model: nn.Module, model_args: ModelArgs, kv_cache: KVCache, device: str,
+                 *, batch_size: int | None = None):
+        if not str(device).startswith("cuda"):
+            raise ValueError("CUDAGraphDecodeRunner requires CUDA device")
+        self.model = model
+        self.model_args = model_args
+        self.kv_cache = kv_cache
+        self.device = device
+        self.batch_size = int(batch_size or model_args.max_batch_size)
+        if self.batch_size > kv_cache.max_batch_size:
+            raise ValueError(f"batch_size {self.batch_size} exceeds the cache's max_batch_size "
+                             f"{kv_cache.max_batch_size}")
+        self.graph = torch.cuda.CUDAGraph()
+        B = self.batch_size
+        self.static_input_token = torch.zeros((B, 1), dtype=torch.long, device=device)
+        self.static_scatter_positions = torch.zeros((1,), dtype=torch.long, device=device)
+        self.static_seq_lens = torch.ones((B,), dtype=torch.long, device=device)
+        self.static_logits = None
+        self._capture()
+
+    def _forward(self):
+        return self.model(self.static_input_token, kv_cache=self.kv_cache, use_cuda_graph=True,
+                          scatter_positions=self.static_scatter_positions,
+                          seq_lens=self.static_seq_lens)
+
+    def _capture(self):
+        torch.cuda.nvtx.range_push("CUDAGraphWarmup")
+        warmup_stream = torch.cuda.Stream(device=self.device)
+        warmup_stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(warmup_stream):
+            self._forward()
+        torch.cuda.current_stream().wait_stream(warmup_stream)
+        torch.cuda.nvtx.range_pop()
+        torch.cuda.nvtx.range_push("CUDAGraphCapture")
+        with torch.cuda.graph(self.graph):
+            self.static_logits = self._forward()
+        torch.cuda.nvtx.range_pop()
+
+    def set_inputs(self, token_id, current_pos: int) -> None:
+        if current_pos >= self.model_args.max_seq_len or current_pos < 0:
+            raise ValueError(f"current_pos out of range: {current_pos}")
+        if isinstance(token_id, torch.Tensor):
+            self.static_input_token.copy_(token_id.reshape(self.batch_size, 1))
+        else:
+            self.static_input_token.fill_(int(token_id))
+        self.static_scatter_positions.fill_(int(current_pos))
+        self.static_seq_lens.fill_(int(current_pos) + 1)
+
+    def replay(self) -> torch.Tensor:
+        self.graph.replay()
+        return self.static_logits
+
+    def decode(self, token_id, current_pos: int) -> torch.Tensor:
+        torch.cuda.nvtx.range_push("CUDAGraphReplay")
+        self.set_inputs(token_id, current_pos)
+        self.graph.replay()
+        torch.cuda.nvtx.range_pop()
+        return self.static_logits

@@ -1,0 +1,89 @@
+"""W8A16 linear layer (interface of src/quant_linear.py).
+
+Int8 weights [N, K] with per-row scales [N, 1]; y = (x.f32 @ q.f32^T) * s in
+fp32, stored in x's dtype.  Decode-sized inputs (M <= 8 rows, the reference's
+threshold at src/quant_linear.py:273) run the MFMA GEMV kernel mi_w8a16_gemv,
+which reads every weight byte once for all rows.  Larger M is served by the
+same kernel in 16-row slices (correct, not tuned for prefill).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+_GEMV_MAX_ROWS = 16
+
+
+def _prep(x, weight, scales):
+    assert x.dim() == 2
+    assert weight.dim() == 2
+    assert weight.dtype == torch.int8
+    assert x.is_cuda and weight.is_cuda and scales.is_cuda
+    assert x.shape[1] == weight.shape[1]
+    N = weight.shape[0]
+    if scales.dim() == 2:
+        assert scales.shape == (N, 1)
+        scales_1d = scales.view(N)
+    else:
+        assert scales.shape == (N,)
+        scales_1d = scales
+    w = weight
+    if w.stride(1) != 1 or w.stride(0) % 16 != 0 or w.data_ptr() % 16 != 0:
+        w = w.contiguous()
+    if x.stride(1) == 1 and (x.data_ptr() % 16 != 0 or (x.stride(0) * x.element_size()) % 16 != 0):
+        x = x.contiguous()
+    return x, w, scales_1d
+
+
+def _gemv_rows(x, w, s, out):
+    M, K = x.shape
+    N = w.shape[0]
+    st = _lib.load().mi_w8a16_gemv(
+        x.data_ptr(), w.data_ptr(), s.data_ptr(), out.data_ptr(), M, N, K,
+        x.stride(0), x.stride(1), w.stride(0), s.stride(0), out.stride(0), out.stride(1),
+        _lib.dtype_code(x.dtype), _lib.dtype_code(s.dtype), _lib.stream_of(x))
+    _lib.check(st, "w8a16_gemv")
+
+
+def w8a16_gemv_launch(x, weight, scales, *, block_n: int = 32, block_k: int = 256):
+    """x [M, K] bf16/fp16, weight [N, K] int8, scales [N, 1] or [N] -> [M, N].
+    block_n/block_k are accepted for signature compatibility (tiling is fixed
+    by the MFMA kernel)."""
+    x, w, s = _prep(x, weight, scales)
+    M = x.shape[0]
+    out = torch.empty((M, w.shape[0]), device=x.device, dtype=x.dtype)
+    for m0 in range(0, M, _GEMV_MAX_ROWS):
+        _gemv_rows(x[m0:m0 + _GEMV_MAX_ROWS], w, s, out[m0:m0 + _GEMV_MAX_ROWS])
+    return out
+
+
+def w8a16_gemm_launch(x, weight, scales, *, block_m: int = 64, block_n: int = 64, block_k: int = 128):
+    """Same contract as w8a16_gemv_launch for any M (src/quant_linear.py:191-247)."""
+    return w8a16_gemv_launch(x, weight, scales)
+
+
+class W8A16Linear(nn.Module):
+    """Per-channel symmetric int8 weight, bf16/fp16 activation linear layer."""
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = False):
+        super().__init__()
+        if bias:
+            raise NotImplementedError("W8A16Linear does not support bias yet.")
+        self.in_features = in_features
+        self.out_features = out_features
+        self.weight = nn.Parameter(torch.empty(out_features, in_features, dtype=torch.int8),
+                                   requires_grad=False)
+        self.scales = nn.Parameter(torch.empty(out_features, 1, dtype=torch.bfloat16),
+                                   requires_grad=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        orig_shape = x.shape
+        x_2d = x.reshape(-1, self.in_features)
+        if x_2d.shape[0] <= 8:
+            out_2d = w8a16_gemv_launch(x_2d, self.weight, self.scales, block_n=32, block_k=256)
+        else:
+            out_2d = w8a16_gemm_launch(x_2d, self.weight, self.scales, block_m=64, block_n=64,
+                                       block_k=128)
+        return out_2d.reshape(*orig_shape[:-1], self.out_features)

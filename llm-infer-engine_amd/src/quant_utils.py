@@ -1,0 +1,40 @@
+"""Symmetric per-channel int8 weight quantisation (interface of
+src/quant_utils.py:7-36), run by one HIP launch (mi_quantize_int8):
+
+    amax  = max(max_k |w[n, k]|, 1e-12)            in fp32
+    scale = (amax / 127) rounded to w's dtype        [N, 1]
+    q     = clamp(round_half_even(w / scale), -128, 127) as int8
+
+Each step is a correctly rounded IEEE operation, so q and scale are bit-exact
+with the reference's torch recipe.
+"""
+from __future__ import annotations
+
+from typing import Tuple
+
+import torch
+
+from . import _lib
+
+
+def quantize_weight_symmetric_per_channel(
+    weight: torch.Tensor,
+    quant_dtype: torch.dtype = torch.int8,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    orig_dtype = weight.dtype
+    if orig_dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError(f"Unsupported weight dtype for quantization: {orig_dtype}")
+    if quant_dtype != torch.int8:
+        raise NotImplementedError("Only int8 symmetric per-channel quantization is supported.")
+    if weight.dim() != 2:
+        raise ValueError(f"weight must be 2-D [out_features, in_features], got {tuple(weight.shape)}")
+    _lib.require_device(weight, "quantize_weight_symmetric_per_channel")
+    w = weight if weight.stride(1) == 1 else weight.contiguous()
+    N, K = w.shape
+    qweight = torch.empty((N, K), dtype=torch.int8, device=w.device)
+    scales = torch.empty((N, 1), dtype=orig_dtype, device=w.device)
+    st = _lib.load().mi_quantize_int8(
+        w.data_ptr(), qweight.data_ptr(), scales.data_ptr(), N, K, w.stride(0),
+        qweight.stride(0), _lib.dtype_code(orig_dtype), _lib.stream_of(w))
+    _lib.check(st, "quantize_weight_symmetric_per_channel")
+    return qweight, scales

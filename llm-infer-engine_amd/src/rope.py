@@ -21,7 +21,7 @@ from . import _lib
 def _compute_inv_freq(dim: int, theta: float, rope_scaling=None):
     """Inverse frequencies 1/theta^(2i/dim) in fp32, with optional llama3
     wavelength-based scaling (src/rope.py:8-30)."""
-    base = 1.0 / (theta ** (torch.arange(0, dim, 2).float() / dim))
+    base = 1.0 / (theta ** (torch.arange(0, dim, 2, device="cpu").float() / dim))
     if not rope_scaling or rope_scaling.get("rope_type") != "llama3":
         return base
     factor = float(rope_scaling["factor"])
@@ -41,7 +41,7 @@ def precompute_freqs_cis(dim: int, end: int, theta: float = 500000.0, rope_scali
     """complex64 [end, dim/2] table exp(i * pos * f) built on the CPU
     (src/rope.py:33-38)."""
     f = _compute_inv_freq(dim=dim, theta=theta, rope_scaling=rope_scaling)
-    angles = torch.outer(torch.arange(end, device=f.device), f).float()
+    angles = torch.outer(torch.arange(end, device="cpu"), f).float()
     return torch.polar(torch.ones_like(angles), angles)
 
 
@@ -78,17 +78,21 @@ def _check_tables(cos: torch.Tensor, sin: torch.Tensor, seq_len: int, head_dim: 
         raise TypeError(f"{what}: cos and sin must share a dtype")
 
 
-def apply_rotary(x, cos, sin):
+def apply_rotary(x, cos, sin, *, positions=None):
     """Rotate-half RoPE of x [B, n_heads, seq_len, head_dim] with cos/sin
     [seq_len, head_dim // 2]; returns a new tensor with x's strides
-    (src/rope.py:94-119)."""
+    (src/rope.py:94-119).  ``positions`` (keyword-only extension, device int64
+    [seq_len]): cos/sin are full tables and token s uses row positions[s]."""
     B, n_heads, seq_len, head_dim = x.shape
     _lib.require_device(x, "apply_rotary")
-    _check_tables(cos, sin, seq_len, head_dim, "apply_rotary")
+    if positions is None:
+        _check_tables(cos, sin, seq_len, head_dim, "apply_rotary")
+    elif positions.dtype != torch.int64 or positions.device != x.device:
+        positions = positions.to(device=x.device, dtype=torch.int64)
     out = torch.empty_like(x)
     lib = _lib.load()
     st = lib.mi_rope(
-        x.data_ptr(), out.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+        x.data_ptr(), out.data_ptr(), cos.data_ptr(), sin.data_ptr(), _lib.ptr(positions),
         B, n_heads, seq_len, head_dim,
         *x.stride(), *out.stride(), *cos.stride(), *sin.stride(),
         _lib.dtype_code(x.dtype), _lib.dtype_code(cos.dtype), _lib.stream_of(x))
