@@ -189,6 +189,40 @@ def bench_decode_cfg4(torch, steps: int, warmup: int) -> dict:
     return out
 
 
+def bench_config5(torch, steps: int, warmup: int) -> dict:
+    """Llama-3.2-1B W8A16 decode step, B8, context 4096, hipGraph replay."""
+    from src.config import ModelArgs
+    from src.cuda_graph import CUDAGraphDecodeRunner
+    from src.kv_cache import KVCache
+    from src.model_quantized import build_random_quantized
+    dev = torch.device("cuda:0")
+    args = ModelArgs(max_batch_size=8, max_seq_len=8192, device=str(dev))
+    model = build_random_quantized(args, seed=0, device=str(dev))
+    kv = KVCache(args, dtype=torch.bfloat16)
+    runner = CUDAGraphDecodeRunner(model, args, kv, str(dev), batch_size=8)
+    g = torch.Generator(device=dev).manual_seed(0)
+    kv.k[:, :, :, :4096].normal_(generator=g)
+    kv.v[:, :, :, :4096].normal_(generator=g)
+    tok = torch.randint(0, args.vocab_size, (8, 1), generator=torch.Generator().manual_seed(0)).to(dev)
+    runner.set_inputs(tok, 4096)
+    ms = _time_graphs(torch, [runner.graph], max(steps, 20), warmup)
+    # int8 linears + bf16 lm_head + K/V read (4097 slots) + scales, per step
+    D, L = 64, 16
+    lin = L * (2048 * 2048 * 2 + 2 * 512 * 2048 + 3 * 2048 * 8192)
+    nbytes = lin + L * (2048 * 2 + 512 * 2 + 8192 * 3) * 2 + 128256 * 2048 * 2 \
+        + L * 8 * 8 * 4097 * D * 2 * 2
+    out = {"config": "5: Llama-3.2-1B random-init W8A16 decode step, B8, ctx 4096, hipGraph",
+           "value": round(8 / (ms * 1e-3), 1), "unit": "tokens/s", "ms_per_step": ms,
+           "bytes": nbytes,
+           "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "traffic": None}}
+    del runner, model, kv
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(torch) -> dict:
     """The fp32 CPU oracle on batch 0 of config 2 (1/4 of a step), on rank 0."""
     from oracle import attention as ora
@@ -220,7 +254,7 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "step"], default=None,
                     help="run one leg only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -239,6 +273,8 @@ def main() -> None:
     if args.only in (None, "decode"):
         extra["decode_config3"] = bench_decode_cfg3(torch, args.steps, args.warmup)
         extra["decode_config4"] = bench_decode_cfg4(torch, args.steps, args.warmup)
+    if args.only in (None, "step"):
+        extra["decode_step_config5"] = bench_config5(torch, args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline and args.only is None:
         cpu = cpu_baseline(torch)
