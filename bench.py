@@ -254,6 +254,8 @@ def main() -> None:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run one plain 1 GiB device copy (scales rocprofv3 FETCH/WRITE_SIZE)")
     ap.add_argument("--only", choices=["prefill", "decode", "step"], default=None,
                     help="run one leg only (profiling)")
     args = ap.parse_args()
@@ -265,6 +267,15 @@ def main() -> None:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        n = 1 << 30
+        src = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n}))
+        return
 
     extra = {}
     pre = None

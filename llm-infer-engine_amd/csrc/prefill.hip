@@ -7,8 +7,9 @@
 //
 // Design (MI355X-first, not a translation of the Triton tile loop):
 //  * A workgroup owns one (batch, kv-head, block of query positions) and runs
-//    one wave per (query head of the GQA group, 32-row slice).  Every K/V tile
-//    is staged in LDS once and consumed by all query heads that share it.
+//    one wave per (query head of the GQA group, 64-row slice).  Every K/V tile
+//    is staged in LDS once and consumed by all query heads that share it; each
+//    wave uses every K/V operand it reads from LDS for two 32-row MFMA blocks.
 //  * Scores are computed transposed, S^T = K Q^T, with
 //    v_mfma_f32_32x32x16_{bf16,f16}: the accumulator layout then gives each
 //    lane all scores of ONE query row (16 per 32-key block), so the row max
@@ -29,6 +30,8 @@
 //    that all blocks of one (batch, kv-head) land on the same XCD, whose L2
 //    then serves the K/V re-reads.
 #include <math.h>
+
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -81,41 +84,60 @@ __device__ inline int perm_row(int r) {
   return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
 }
 
-template <typename T, int D>
-struct PrefillGeom {
-  static constexpr int kBN = 64;             // keys per tile
-  static constexpr int kKCH = D / 8;         // 16-byte chunks per K row
-  static constexpr int kDC = D / 16;         // MFMA k-steps over the head dim
-  static constexpr int kDB = D / 32;         // 32-row blocks of O^T
-  static constexpr int kKTile = kBN * D;     // elements per K tile
-  static constexpr int kVTile = D * kBN;     // elements per V^T tile
-  static constexpr int kKUnits = kBN * kKCH;         // 16B chunks per K tile
-  static constexpr int kVUnits = (kBN / 2) * kKCH;   // (key pair, chunk) units
-  static constexpr int kMinThreads = 256;            // blocks are 4 waves
-  static constexpr int kKPer = (kKUnits + kMinThreads - 1) / kMinThreads;
-  static constexpr int kVPer = (kVUnits + kMinThreads - 1) / kMinThreads;
-  static constexpr size_t kSmem = 2 * (size_t)(kKTile + kVTile) * sizeof(T);
-};
 
-// physical 16-byte chunk of logical chunk c in K row r / V^T row d
+// LDS tile layouts (one buffer): K [BN][D] and V [BN][D], both row-major in
+// 16-byte chunks with the chunk index XOR-swizzled per row.  Tiles are filled
+// by global->LDS DMA (global_load_lds_dwordx4): a wave instruction writes 1 KB
+// contiguously, lane t at +16t, so the swizzle is realised by choosing which
+// logical chunk each lane fetches.
 template <int D>
-__device__ inline int k_swz(int r, int c) {
-  if constexpr (D == 64) return c ^ ((r >> 1) & 7);
-  else return c ^ (r & 15);
+__device__ inline int k_swz(int r) {  // XOR mask for K row r
+  if constexpr (D == 64) return (r >> 1) & 7;
+  else return r & 15;
 }
-__device__ inline int vt_swz(int d, int kc) { return kc ^ ((d >> 1) & 7); }
+__device__ inline int v_swz(int r) { return (r >> 1) & 3; }  // XOR mask for V row r
+
+// Online-softmax rescale threshold (log2 units): the running row max used for
+// exp2 is only moved when a new score exceeds it by more than this, so
+// probabilities stay <= 2^8 (exact maths is unchanged: O and l share the same
+// reference max) and O is rescaled on rare tiles instead of on every tile.
+constexpr float kRescaleThreshold = 8.0f;
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline void lds_dma16(const void* g, unsigned char* l) {
+  __builtin_amdgcn_global_load_lds(g, l, 16, 0, 0);
+}
+__device__ inline void dma_wait_all() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Transposed 64-bit LDS read: within each 16-lane group, lane i receives
+// element (i % 4) of the 8-byte chunks addressed by lanes 4e + i/4, e = 0..3.
+__device__ inline uint2 lds_read_tr(const unsigned char* p) {
+  s16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
+// Each wave owns RB blocks of 32 query rows (RB = 2 at D = 64):
+// every K / V operand read from LDS feeds two MFMAs, and the two row blocks are
+// independent instruction streams the scheduler interleaves (the softmax VALU
+// of one block runs while the other's MFMAs execute).
+template <int D>
+constexpr int prefill_row_blocks() { return D == 64 ? 2 : 1; }  // D=128: registers
 
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
-  using Geo = PrefillGeom<T, D>;
   using MM = Mfma<T>;
   typedef typename MM::v8 v8;
-  constexpr int BN = Geo::kBN, KCH = Geo::kKCH, DC = Geo::kDC, DB = Geo::kDB;
+  constexpr int BN = 64, KCH = D / 8, DC = D / 16, DB = D / 32, RB = prefill_row_blocks<D>();
+  constexpr int ROW_B = D * 2;                  // bytes per K/V row
+  constexpr int TILE_B = BN * ROW_B;            // bytes per K or V tile
+  constexpr int NI = TILE_B / 1024 / 4;         // DMA instructions per wave per tile
+  static_assert(NI * 4 * 1024 == TILE_B, "tile must split into 1 KB wave copies");
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  T* k_lds = reinterpret_cast<T*>(smem_raw);            // [2][BN][D]
-  T* vt_lds = k_lds + 2 * Geo::kKTile;                  // [2][D][BN]
+  unsigned char* const lds = smem_raw;          // [2][K tile | V tile]
 
-  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int hh = lane >> 5, lr = lane & 31;
 
@@ -137,209 +159,228 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   const int kvh = (pair / a.head_chunks) % a.Hkv;
   const int b = pair / (a.head_chunks * a.Hkv);
   const int GH = a.heads_per_block;
-  const int rows_pb = 32 * a.pj;
+  const int rows_pb = 32 * RB * a.pj;
   const int p0 = pb * rows_pb;
 
   const int g = w % GH, j = w / GH;
   const int head = kvh * a.G + hc * GH + g;
-  const int qpos0 = p0 + 32 * j;          // first query row of this wave
-  const int qrow = qpos0 + lr;            // this lane's query row
+  const int qpos0 = p0 + 32 * RB * j;     // first query row of this wave
   const bool wave_active = qpos0 < a.S;
 
-  // ---- Q as the B operand of S^T = K Q^T (lane: row lr, 8 dims per k-step)
-  v8 qreg[DC];
-  {
+  // ---- Q as the B operand of S^T = K Q^T (lane: row lr of each row block)
+  v8 qreg[RB][DC];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int qrow = qpos0 + 32 * rb + lr;
     const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
                   (int64_t)head * a.q_sh + (int64_t)min(qrow, a.S - 1) * a.q_ss;
 #pragma unroll
     for (int c = 0; c < DC; ++c) {
       u32x4 raw = load16(qp + 16 * c + 8 * hh);
       if (qrow >= a.S) raw = u32x4{0, 0, 0, 0};
-      qreg[c] = __builtin_bit_cast(v8, raw);
+      qreg[rb][c] = __builtin_bit_cast(v8, raw);
     }
   }
 
-  const T* kbase = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh;
-  const T* vbase = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh;
+  // ---- DMA geometry: wave w copies 1 KB pieces (w*NI + i) of each tile
+  const unsigned char* kbase = reinterpret_cast<const unsigned char*>(a.k) +
+                               ((int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh) * 2;
+  const unsigned char* vbase = reinterpret_cast<const unsigned char*>(a.v) +
+                               ((int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh) * 2;
+  int dma_row[NI];
+  uint32_t k_goff[NI], v_goff[NI];
+  int k_lc[NI], v_lc[NI];
+#pragma unroll
+  for (int i = 0; i < NI; ++i) {
+    const int idx = (w * NI + i) * 64 + lane;   // physical chunk index in the tile
+    const int r = idx / KCH, pc = idx % KCH;
+    dma_row[i] = r;
+    k_lc[i] = pc ^ k_swz<D>(r);                 // logical chunk this lane fetches
+    v_lc[i] = pc ^ v_swz(r);
+    k_goff[i] = (uint32_t)(r * a.k_ss + k_lc[i] * 8) * 2u;
+    v_goff[i] = (uint32_t)(r * a.v_ss + v_lc[i] * 8) * 2u;
+  }
+  auto issue = [&](int kt, int buf) {
+    const int r0 = kt * BN;
+    unsigned char* kl = lds + buf * (2 * TILE_B);
+    unsigned char* vl = kl + TILE_B;
+    const unsigned char* kt_base = kbase + (int64_t)r0 * a.k_ss * 2;
+    const unsigned char* vt_base = vbase + (int64_t)r0 * a.v_ss * 2;
+    if (r0 + BN <= a.S) {
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        lds_dma16(kt_base + k_goff[i], kl + (w * NI + i) * 1024);
+        lds_dma16(vt_base + v_goff[i], vl + (w * NI + i) * 1024);
+      }
+    } else {  // last, partial tile: rows clamped to S-1 (masked out later)
+      const int lim = a.S - 1 - r0;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int r = min(dma_row[i], lim);
+        lds_dma16(kt_base + (uint32_t)(r * a.k_ss + k_lc[i] * 8) * 2u, kl + (w * NI + i) * 1024);
+        lds_dma16(vt_base + (uint32_t)(r * a.v_ss + v_lc[i] * 8) * 2u, vl + (w * NI + i) * 1024);
+      }
+    }
+  };
+
+  // ---- per-lane operand read offsets (bytes, within one buffer)
+  const int prow = perm_row(lr);
+  int k_rd[DC];
+#pragma unroll
+  for (int c = 0; c < DC; ++c) k_rd[c] = prow * ROW_B + (((2 * c + hh) ^ k_swz<D>(prow)) * 16);
+  const int gq = lane >> 4, sl = lane & 15;
+  int v_rd[8];
+#pragma unroll
+  for (int q8 = 0; q8 < 8; ++q8) {  // q8 = 4*sb + 2*cc + half
+    const int sb = q8 >> 2, cc = (q8 >> 1) & 1, half = q8 & 1;
+    const int r = 32 * sb + 16 * cc + 8 * (gq >> 1) + 4 * half + (sl >> 2);
+    const int d0 = 16 * (gq & 1) + 4 * (sl & 3);  // db = 0; db adds 32 dims = 4 chunks
+    v_rd[q8] = r * ROW_B + (((d0 >> 3) ^ v_swz(r)) * 16) + (d0 & 7) * 2;
+  }
+
   const int last_row = min(p0 + rows_pb, a.S) - 1;
   const int n_tiles = last_row / BN + 1;
 
-  u32x4 kpre[Geo::kKPer];
-  u32x4 vpre[Geo::kVPer][2];
-
-  auto fetch = [&](int kt) {
-    const int r0 = kt * BN;
+  f32x16 o[RB][DB];
 #pragma unroll
-    for (int i = 0; i < Geo::kKPer; ++i) {
-      const int u = tid + i * nthr;
-      if (u < Geo::kKUnits) {
-        const int r = u / KCH, c = u % KCH;
-        const int row = min(r0 + r, a.S - 1);
-        kpre[i] = load16(kbase + (int64_t)row * a.k_ss + c * 8);
-      }
-    }
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
-    for (int i = 0; i < Geo::kVPer; ++i) {
-      const int u = tid + i * nthr;
-      if (u < Geo::kVUnits) {
-        const int kp = u / KCH, c = u % KCH;
-        const int row0 = min(r0 + 2 * kp, a.S - 1), row1 = min(r0 + 2 * kp + 1, a.S - 1);
-        vpre[i][0] = load16(vbase + (int64_t)row0 * a.v_ss + c * 8);
-        vpre[i][1] = load16(vbase + (int64_t)row1 * a.v_ss + c * 8);
-      }
-    }
-  };
-  auto stash = [&](int buf) {
-    T* kl = k_lds + buf * Geo::kKTile;
-    T* vl = vt_lds + buf * Geo::kVTile;
+    for (int db = 0; db < DB; ++db)
 #pragma unroll
-    for (int i = 0; i < Geo::kKPer; ++i) {
-      const int u = tid + i * nthr;
-      if (u < Geo::kKUnits) {
-        const int r = u / KCH, c = u % KCH;
-        *reinterpret_cast<u32x4*>(kl + r * D + k_swz<D>(r, c) * 8) = kpre[i];
-      }
-    }
+      for (int i = 0; i < 16; ++i) o[rb][db][i] = 0.f;
+  float m[RB], l[RB];
 #pragma unroll
-    for (int i = 0; i < Geo::kVPer; ++i) {
-      const int u = tid + i * nthr;
-      if (u < Geo::kVUnits) {
-        const int kp = u / KCH, c = u % KCH;
-        const uint32_t w0[4] = {vpre[i][0].x, vpre[i][0].y, vpre[i][0].z, vpre[i][0].w};
-        const uint32_t w1[4] = {vpre[i][1].x, vpre[i][1].y, vpre[i][1].z, vpre[i][1].w};
-        const int kc = kp >> 2, kw = kp & 3;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int d = 8 * c + jj;
-          const uint32_t sel = (jj & 1) ? 0x07060302u : 0x05040100u;
-          const uint32_t word = __builtin_amdgcn_perm(w1[jj >> 1], w0[jj >> 1], sel);
-          uint32_t* dst = reinterpret_cast<uint32_t*>(vl + d * BN + vt_swz(d, kc) * 8) + kw;
-          *dst = word;
-        }
-      }
-    }
-  };
-
-  f32x16 o[DB];
-#pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) o[db][i] = 0.f;
-  float m = kNegBig, l = 0.f;
+  for (int rb = 0; rb < RB; ++rb) { m[rb] = kNegBig; l[rb] = 0.f; }
   const float sl2 = a.scale_log2;
-  const int prow = perm_row(lr);
 
-  fetch(0);
-  stash(0);
+  issue(0, 0);
+  dma_wait_all();
   __syncthreads();
 
-  for (int kt = 0; kt < n_tiles; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < n_tiles) fetch(kt + 1);
-
-    const int kbase_pos = kt * BN;
-    if (wave_active && kbase_pos <= qpos0 + 31) {
-      const T* kl = k_lds + buf * Geo::kKTile;
-      const T* vl = vt_lds + buf * Geo::kVTile;
-      f32x16 s[2];
+  auto tile = [&](int kt, auto buf_c) {
+    constexpr int buf = decltype(buf_c)::value;
+    if (kt + 1 < n_tiles) issue(kt + 1, buf ^ 1);
+    const int kpos = kt * BN;
+    if (wave_active && kpos <= qpos0 + 32 * RB - 1) {
+      const unsigned char* kl = lds + buf * (2 * TILE_B);
+      const unsigned char* vl = kl + TILE_B;
+      // S^T for both row blocks: each K operand read feeds two MFMAs
+      f32x16 s[RB][2];
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s[sb][i] = 0.f;
-        const int r = 32 * sb + prow;
-#pragma unroll
-        for (int c = 0; c < DC; ++c) {
-          const v8 kv = __builtin_bit_cast(
-              v8, *reinterpret_cast<const u32x4*>(kl + r * D + k_swz<D>(r, 2 * c + hh) * 8));
-          s[sb] = MM::mma(kv, qreg[c], s[sb]);
-        }
-      }
-      // causal mask (keys > query row, which also covers keys >= S)
-      if (kbase_pos + BN - 1 > qpos0) {
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = kbase_pos + 32 * sb + 16 * (i >> 3) + 8 * hh + (i & 7);
-            if (key > qrow) s[sb][i] = -INFINITY;
-          }
-      }
-      float mx = s[0][0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[0][i]);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[1][i]);
-      {
-        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-        mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-      }
-      const float m_new = fmaxf(m, mx * sl2);
-      const float alpha = fast_exp2(m - m_new);
-      m = m_new;
-      v8 pb[2][2];
-      float ls = 0.f;
+          for (int i = 0; i < 16; ++i) s[rb][sb][i] = 0.f;
 #pragma unroll
       for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
+        for (int c = 0; c < DC; ++c) {
+          const v8 ka = __builtin_bit_cast(
+              v8, *reinterpret_cast<const u32x4*>(kl + k_rd[c] + sb * 32 * ROW_B));
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) s[rb][sb] = MM::mma(ka, qreg[rb][c], s[rb][sb]);
+        }
+      v8 pb[RB][4];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const int r0 = qpos0 + 32 * rb;
+        if (kpos + BN - 1 > r0) {  // diagonal tile for this row block
+          const int rel = r0 + lr - kpos - 8 * hh;  // visible iff key offset <= rel
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int kk = 16 * (i >> 3) + (i & 7);
+            if (kk > rel) s[rb][0][i] = -INFINITY;
+            if (kk + 32 > rel) s[rb][1][i] = -INFINITY;
+          }
+        }
+        float mx = fmaxf(s[rb][0][0], s[rb][0][1]);
+#pragma unroll
+        for (int i = 2; i < 16; i += 2) mx = fmaxf(mx, fmaxf(s[rb][0][i], s[rb][0][i + 1]));
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(s[rb][1][i], s[rb][1][i + 1]));
+        {
+          auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+          mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl2;
+        }
+        if (__builtin_amdgcn_ballot_w64(mx > m[rb] + kRescaleThreshold) != 0) {
+          const float m_new = fmaxf(m[rb], mx);
+          const float alpha = fast_exp2(m[rb] - m_new);
+          m[rb] = m_new;
+          l[rb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[rb][db][i] *= alpha;
+        }
+        const float mr = m[rb];
+        float ls0 = 0.f, ls1 = 0.f;
+#pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-          uint32_t wds[4];
+          uint32_t w0[4], w1[4];
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            const float p0v = fast_exp2(fmaf(s[sb][8 * cc + 2 * t], sl2, -m_new));
-            const float p1v = fast_exp2(fmaf(s[sb][8 * cc + 2 * t + 1], sl2, -m_new));
-            wds[t] = MM::pack2(p0v, p1v);
-            ls += p0v + p1v;
+            const float a0 = fast_exp2(fmaf(s[rb][0][8 * cc + 2 * t], sl2, -mr));
+            const float a1 = fast_exp2(fmaf(s[rb][0][8 * cc + 2 * t + 1], sl2, -mr));
+            const float b0 = fast_exp2(fmaf(s[rb][1][8 * cc + 2 * t], sl2, -mr));
+            const float b1 = fast_exp2(fmaf(s[rb][1][8 * cc + 2 * t + 1], sl2, -mr));
+            ls0 += a0 + a1;
+            ls1 += b0 + b1;
+            w0[t] = MM::pack2(a0, a1);
+            w1[t] = MM::pack2(b0, b1);
           }
-          pb[sb][cc] = __builtin_bit_cast(v8, u32x4{wds[0], wds[1], wds[2], wds[3]});
+          pb[rb][cc] = __builtin_bit_cast(v8, u32x4{w0[0], w0[1], w0[2], w0[3]});
+          pb[rb][2 + cc] = __builtin_bit_cast(v8, u32x4{w1[0], w1[1], w1[2], w1[3]});
         }
-      l = l * alpha + ls;
+        l[rb] += ls0 + ls1;
+      }
+      // O^T += V^T P^T: each V operand read feeds both row blocks
 #pragma unroll
-      for (int db = 0; db < DB; ++db)
+      for (int q4 = 0; q4 < 4; ++q4)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        for (int db = 0; db < DB; ++db) {
+          const uint2 lo = lds_read_tr(vl + v_rd[2 * q4] + db * 64);
+          const uint2 hi = lds_read_tr(vl + v_rd[2 * q4 + 1] + db * 64);
+          const v8 vv = __builtin_bit_cast(v8, u32x4{lo.x, lo.y, hi.x, hi.y});
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-          const int kc = 4 * sb + 2 * cc + hh;  // 8-key chunk of this lane's keys
-#pragma unroll
-          for (int db = 0; db < DB; ++db) {
-            const int d = 32 * db + lr;
-            const v8 vv = __builtin_bit_cast(
-                v8, *reinterpret_cast<const u32x4*>(vl + d * BN + vt_swz(d, kc) * 8));
-            o[db] = MM::mma(vv, pb[sb][cc], o[db]);
-          }
+          for (int rb = 0; rb < RB; ++rb) o[rb][db] = MM::mma(vv, pb[rb][q4], o[rb][db]);
         }
     }
-
-    if (kt + 1 < n_tiles) stash(buf ^ 1);
+    dma_wait_all();
     __syncthreads();
+  };
+  for (int kt = 0; kt < n_tiles; kt += 2) {
+    tile(kt, std::integral_constant<int, 0>{});
+    if (kt + 1 < n_tiles) tile(kt + 1, std::integral_constant<int, 1>{});
   }
 
   if (!wave_active) return;
-  // both lane halves hold partial sums of the same row
-  {
-    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false, false);
-    l = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-  }
-  if (qrow >= a.S) return;
-  const float inv = 1.0f / l;
-  T* op = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_sb + (int64_t)head * a.o_sh +
-          (int64_t)qrow * a.o_ss;
 #pragma unroll
-  for (int db = 0; db < DB; ++db)
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int d = 32 * db + 8 * q4 + 4 * hh;
-      const uint32_t w0 = MM::pack2(o[db][4 * q4] * inv, o[db][4 * q4 + 1] * inv);
-      const uint32_t w1 = MM::pack2(o[db][4 * q4 + 2] * inv, o[db][4 * q4 + 3] * inv);
-      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-      *reinterpret_cast<u32x2*>(op + d) = u32x2{w0, w1};
+  for (int rb = 0; rb < RB; ++rb) {
+    float lt = l[rb];
+    {  // both lane halves hold partial sums of the same row
+      auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lt), __float_as_uint(lt), false, false);
+      lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
-  if (a.lse != nullptr && hh == 0)
-    a.lse[((int64_t)b * a.Hq + head) * a.S + qrow] = (m + __log2f(l)) * kLn2;
+    const int qrow = qpos0 + 32 * rb + lr;
+    if (qrow >= a.S) continue;
+    const float inv = 1.0f / lt;
+    T* op = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_sb + (int64_t)head * a.o_sh +
+            (int64_t)qrow * a.o_ss;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = 32 * db + 8 * q4 + 4 * hh;
+        const uint32_t w0 = MM::pack2(o[rb][db][4 * q4] * inv, o[rb][db][4 * q4 + 1] * inv);
+        const uint32_t w1 = MM::pack2(o[rb][db][4 * q4 + 2] * inv, o[rb][db][4 * q4 + 3] * inv);
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u32x2*>(op + d) = u32x2{w0, w1};
+      }
+    if (a.lse != nullptr && hh == 0)
+      a.lse[((int64_t)b * a.Hq + head) * a.S + qrow] = (m[rb] + __log2f(lt)) * kLn2;
+  }
 }
-
 
 // fp32 inputs: plain VALU flash attention (no fp32 MFMA tiles), TPR = D/32
 // lanes per query row, 32 dims each; K/V tiles of 64 keys staged in LDS and
@@ -405,11 +446,11 @@ namespace {
 
 template <typename T, int D>
 hipError_t launch(const PrefillArgs& a, int nwaves, hipStream_t stream) {
-  using Geo = PrefillGeom<T, D>;
   const int n_pairs = a.B * a.Hkv * a.head_chunks;
   dim3 grid((unsigned)(n_pairs * a.n_pb));
   dim3 block((unsigned)(nwaves * 64));
-  hipLaunchKernelGGL((prefill_kernel<T, D>), grid, block, Geo::kSmem, stream, a);
+  const size_t smem = 2 * 2 * 64 * D * sizeof(T);  // 2 buffers x (K + V) tiles
+  hipLaunchKernelGGL((prefill_kernel<T, D>), grid, block, smem, stream, a);
   return hipGetLastError();
 }
 
@@ -463,13 +504,20 @@ extern "C" int32_t mi_attn_prefill(const void* q, const void* k, const void* v,
     set_last_error("attn_prefill: rows must be 16-byte aligned with unit head-dim stride");
     return MI_ERR_INVALID;
   }
+  // tile loads use 32-bit byte offsets from a per-tile base
+  if ((k_ss > 0 ? k_ss : -k_ss) * 64 * eb + head_dim * eb >= ((int64_t)1 << 31) ||
+      (v_ss > 0 ? v_ss : -v_ss) * 64 * eb + head_dim * eb >= ((int64_t)1 << 31) ||
+      k_ss <= 0 || v_ss <= 0) {
+    set_last_error("attn_prefill: K/V row stride out of range for 32-bit tile offsets");
+    return MI_ERR_UNSUPPORTED;
+  }
   if (seq_len > (1 << 30) || batch * n_kv_heads * n_heads > (1 << 30)) {
     set_last_error("attn_prefill: shape exceeds launch limits");
     return MI_ERR_UNSUPPORTED;
   }
   const int G = (int)(n_heads / n_kv_heads);
-  // 4 waves per block: 4 query heads x 32 rows, 2 heads x 64 rows or
-  // 1 head x 128 rows, whichever divides the GQA group size.
+  // 4 waves per block, each 32*RB query rows of one head: 4 query heads, 2
+  // heads x 2 slices or 1 head x 4 slices, whichever divides the group size.
   const int gh = (G % 4 == 0) ? 4 : (G % 2 == 0) ? 2 : 1;
   const int pj = 4 / gh;
   PrefillArgs a{};
@@ -483,7 +531,8 @@ extern "C" int32_t mi_attn_prefill(const void* q, const void* k, const void* v,
   a.heads_per_block = gh;
   a.head_chunks = G / gh;
   a.pj = pj;
-  a.n_pb = (int32_t)((seq_len + 32 * pj - 1) / (32 * pj));
+  const int rows_per_wave = 32 * (head_dim == 64 ? prefill_row_blocks<64>() : prefill_row_blocks<128>());
+  a.n_pb = (int32_t)((seq_len + rows_per_wave * pj - 1) / (rows_per_wave * pj));
   a.scale_log2 = sm_scale * kLog2e;
   const int nwaves = gh * pj;
   const int64_t blocks = (int64_t)a.B * a.Hkv * a.head_chunks * a.n_pb;
