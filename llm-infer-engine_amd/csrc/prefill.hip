@@ -7,9 +7,10 @@
 //
 // Design (MI355X-first, not a translation of the Triton tile loop):
 //  * A workgroup owns one (batch, kv-head, block of query positions) and runs
-//    one wave per (query head of the GQA group, 64-row slice).  Every K/V tile
-//    is staged in LDS once and consumed by all query heads that share it; each
-//    wave uses every K/V operand it reads from LDS for two 32-row MFMA blocks.
+//    one wave per (query head of the GQA group, row slice).  Every K/V tile is
+//    copied into LDS once (global->LDS DMA, no register round trip) and read
+//    by all query heads that share it; each wave uses every K/V operand it
+//    reads from LDS for two 32-row MFMA blocks.
 //  * Scores are computed transposed, S^T = K Q^T, with
 //    v_mfma_f32_32x32x16_{bf16,f16}: the accumulator layout then gives each
 //    lane all scores of ONE query row (16 per 32-key block), so the row max
@@ -17,15 +18,16 @@
 //  * The K rows feeding the MFMA are permuted (bits 2 and 3 of the row index
 //    swapped) so that the bf16-converted P^T accumulator is directly the B
 //    operand of O^T = V^T P^T: no register shuffles between the two products.
-//  * V is written to LDS transposed (V^T, key-contiguous) so each lane reads
-//    its A operand with one 16-byte ds_read; K and V^T rows use XOR swizzles
-//    of the 16-byte chunk index to spread LDS banks.
+//  * V stays key-major in LDS; the V^T operand is read with the transposing
+//    ds_read_b64_tr_b16.  K and V rows use XOR swizzles of the 16-byte chunk
+//    index to spread LDS banks.
 //  * Online softmax in fp32 registers in the log2 domain (v_exp_f32), scale
 //    folded into one FMA per score; the row sum is taken over fp32 P and P is
 //    rounded to the input dtype only for the PV product (as the reference does,
 //    src/flash_attn.py:63,72).
-//  * Double-buffered LDS tiles with the next tile's global loads in flight
-//    during the current tile's MFMAs; one barrier per tile.
+//  * head_dim 64: a software-pipelined kernel (each wave overlaps its own
+//    MFMAs with its softmax, 4-slot LDS ring, one barrier per tile);
+//    head_dim 128: double-buffered tiles, one barrier per tile.
 //  * Blocks are ordered heaviest-first (longest causal prefix) and mapped so
 //    that all blocks of one (batch, kv-head) land on the same XCD, whose L2
 //    then serves the K/V re-reads.
@@ -430,41 +432,51 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// Ping-pong variant (D = 64).  A wave issues instructions in order, so its own
-// MFMAs and softmax VALU work run one after the other; the matrix core and the
-// VALU of a SIMD do run side by side when the two streams come from different
-// waves.  This kernel therefore runs 8 waves per block in two groups of four
-// (wave w on SIMD w % 4, so every SIMD holds one wave of each group) and
-// alternates them with block barriers: while group A issues the MFMAs of
-// PV(t-1) + QK(t), group B runs the softmax of its tile t-1, then the roles
-// swap.  Tiles live in a 3-slot LDS ring: tile t is read during four
-// consecutive phases (QK by A then B, PV by A then B), and the copy of tile
-// t+1 is issued two phases before it is needed.
-constexpr int kPpSlots = 3;
-
 __device__ inline void block_sync_lds() {
   // LDS reads of this wave are complete and every wave has arrived; the
   // tile copies (vmcnt) are waited for separately where a tile is published.
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-template <typename T, int D>
-__global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillArgs a) {
+// ---------------------------------------------------------------------------
+// Software-pipelined variant (D = 64, 16-bit).  At D = 64 the softmax VALU work
+// of a tile (one exp, fma, add per score plus the row max and packing) issues
+// for about as long as its MFMAs take to execute, and a wave issues its VALU
+// instructions one at a time.  Each wave therefore overlaps its own matrix and
+// vector work: keys are processed in 32-key halves, and while the softmax of
+// half u runs on the VALU, the same wave has the MFMAs of half u+1 (S^T =
+// K Q^T) and half u-1 (O^T += V^T P^T) in flight.  Two 4-wave blocks share a
+// CU (two waves per SIMD, not coupled by barriers), so the SIMD can co-issue
+// VALU work of one wave while the other's MFMAs execute.
+//
+//   slot A(t): softmax(t.h0) | PV(t-1.h1), QK(t.h1)
+//   ---- wait for tile t+1, barrier, copy tile t+3 into the ring ----
+//   slot B(t): softmax(t.h1) | PV(t.h0),   QK(t+1.h0)
+//
+// Tile t is read in slots B(t-1), A(t), B(t), A(t+1); the 4-slot LDS ring lets
+// the copy of tile t+3 start right after A(t), two slots before its first use.
+// A wave owns 64 query rows (two 32-row MFMA blocks that share every K and V
+// operand read from LDS); every key tile is visible in full except the wave's
+// last (diagonal) tile, whose first half masks row block 0 with the causal
+// triangle and whose second half is invisible to row block 0 and masks row
+// block 1.  The online-softmax rescale is decided once per half for the wave
+// (the max is only moved past the threshold, so it is rare) and applied in a
+// branch after the half's MFMAs are issued.
+constexpr int kSpBufs = 4;
+
+template <typename T>
+__global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
   using MM = Mfma<T>;
   typedef typename MM::v8 v8;
-  constexpr int BN = 64, KCH = D / 8, DC = D / 16, DB = D / 32, RB = 2;
-  constexpr int ROW_B = D * 2;                  // bytes per K/V row
-  constexpr int TILE_B = BN * ROW_B;            // bytes per K or V tile
-  constexpr int SLOT_B = 2 * TILE_B;            // K tile | V tile
-  constexpr int NI = TILE_B / 1024 / 8;         // 1 KB copies per wave per K (V) tile
-  static_assert(NI >= 1 && NI * 8 * 1024 == TILE_B, "tile must split into 1 KB wave copies");
+  constexpr int D = 64, BN = 64, KCH = D / 8, DC = D / 16;
+  constexpr int ROW_B = D * 2, TILE_B = BN * ROW_B, SLOT_B = 2 * TILE_B;
+  constexpr int NI = TILE_B / 1024 / 4;        // 1 KB copies per wave per K (V) tile
+  static_assert(NI * 4 * 1024 == TILE_B, "tile must split into 1 KB wave copies");
   extern __shared__ __align__(16) unsigned char smem_raw[];
   unsigned char* const lds = smem_raw;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
-  const int grp = w >> 2, wi = w & 3;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hh = lane >> 5, lr = lane & 31;
 
   // ---- block -> (batch, kv head, head chunk, position block), heavy first,
@@ -485,19 +497,18 @@ __global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillArgs a) {
   const int kvh = (pair / a.head_chunks) % a.Hkv;
   const int b = pair / (a.head_chunks * a.Hkv);
   const int GH = a.heads_per_block, PJ = a.pj;
-  const int rows_pb = 2 * 32 * RB * PJ;         // two groups of PJ 64-row slices
-  const int p0 = pb * rows_pb;
-
-  const int g = wi % GH, j = wi / GH;
+  const int p0 = pb * 64 * PJ;
+  const int g = w % GH, j = w / GH;
   const int head = kvh * a.G + hc * GH + g;
-  const int qpos0 = p0 + 32 * RB * (grp * PJ + j);  // first query row of this wave
-  const bool wave_active = qpos0 < a.S;
+  const int r0 = p0 + 64 * j;                        // first query row of this wave
+  const int n_tw = r0 < a.S ? r0 / BN + 1 : 0;       // tiles this wave reads (last = diagonal)
+  const int n_tiles = (min(p0 + 64 * PJ, a.S) - 1) / BN + 1;  // tiles the block copies
 
   // ---- Q as the B operand of S^T = K Q^T (lane: row lr of each row block)
-  v8 qreg[RB][DC];
+  v8 qreg[2][DC];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int qrow = qpos0 + 32 * rb + lr;
+  for (int rb = 0; rb < 2; ++rb) {
+    const int qrow = r0 + 32 * rb + lr;
     const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
                   (int64_t)head * a.q_sh + (int64_t)min(qrow, a.S - 1) * a.q_ss;
 #pragma unroll
@@ -513,230 +524,242 @@ __global__ __launch_bounds__(512, 1) void prefill_pp_kernel(PrefillArgs a) {
                                ((int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh) * 2;
   const unsigned char* vbase = reinterpret_cast<const unsigned char*>(a.v) +
                                ((int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh) * 2;
-  int dma_row[NI], k_lc[NI], v_lc[NI];
-  uint32_t k_goff[NI], v_goff[NI];
-#pragma unroll
-  for (int i = 0; i < NI; ++i) {
-    const int idx = (w * NI + i) * 64 + lane;   // physical chunk index in the tile
-    const int r = idx / KCH, pc = idx % KCH;
-    dma_row[i] = r;
-    k_lc[i] = pc ^ k_swz<D>(r);                 // logical chunk this lane fetches
-    v_lc[i] = pc ^ v_swz(r);
-    k_goff[i] = (uint32_t)(r * a.k_ss + k_lc[i] * 8) * 2u;
-    v_goff[i] = (uint32_t)(r * a.v_ss + v_lc[i] * 8) * 2u;
-  }
   const uint32_t lds0 = lds_addr(lds) + w * NI * 1024;
-  auto issue = [&](int t, int slot) {
-    const int r0 = t * BN;
-    const uint32_t kl = lds0 + slot * SLOT_B, vl = kl + TILE_B;
-    const unsigned char* kt_base = kbase + (int64_t)r0 * a.k_ss * 2;
-    const unsigned char* vt_base = vbase + (int64_t)r0 * a.v_ss * 2;
-    if (r0 + BN <= a.S) {
+  // Copy tile t into ring slot t % kSpBufs.  The lane -> chunk geometry is
+  // recomputed here (a few integer ops per tile) rather than kept in registers.
+  auto issue = [&](int t) {
+    const int r0t = t * BN;
+    const uint32_t kl = lds0 + (t % kSpBufs) * SLOT_B, vl = kl + TILE_B;
+    const unsigned char* kt_base = kbase + (int64_t)r0t * a.k_ss * 2;
+    const unsigned char* vt_base = vbase + (int64_t)r0t * a.v_ss * 2;
+    const int lim = a.S - 1 - r0t;   // rows past S are clamped (masked out later)
 #pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        lds_dma16(kt_base, k_goff[i], kl + i * 1024);
-        lds_dma16(vt_base, v_goff[i], vl + i * 1024);
-      }
-    } else {  // last, partial tile: rows clamped to S-1 (masked out later)
-      const int lim = a.S - 1 - r0;
-#pragma unroll
-      for (int i = 0; i < NI; ++i) {
-        const int r = min(dma_row[i], lim);
-        lds_dma16(kt_base, (uint32_t)(r * a.k_ss + k_lc[i] * 8) * 2u, kl + i * 1024);
-        lds_dma16(vt_base, (uint32_t)(r * a.v_ss + v_lc[i] * 8) * 2u, vl + i * 1024);
-      }
+    for (int i = 0; i < NI; ++i) {
+      const int idx = (w * NI + i) * 64 + lane;   // physical chunk index in the tile
+      const int r = idx / KCH, pc = idx % KCH;
+      const int rr = min(r, lim);
+      lds_dma16(kt_base, (uint32_t)(rr * a.k_ss + (pc ^ k_swz<D>(r)) * 8) * 2u, kl + i * 1024);
+      lds_dma16(vt_base, (uint32_t)(rr * a.v_ss + (pc ^ v_swz(r)) * 8) * 2u, vl + i * 1024);
     }
   };
 
-  // ---- per-lane operand read offsets (bytes, within one slot)
+  // ---- per-lane operand read offsets (bytes, within one ring slot)
   const int prow = perm_row(lr);
   int k_rd[DC];
 #pragma unroll
   for (int c = 0; c < DC; ++c) k_rd[c] = prow * ROW_B + (((2 * c + hh) ^ k_swz<D>(prow)) * 16);
+  // V^T operand rows r = 32*half + 16*cc + 8*(gq>>1) + 4*part + (sl>>2): the
+  // swizzle (r>>1)&3 depends only on `part` and the lane, so two base offsets
+  // plus immediates address every read.
   const int gq = lane >> 4, sl = lane & 15;
-  int v_rd[8];
+  int v_rd[2];
 #pragma unroll
-  for (int q8 = 0; q8 < 8; ++q8) {  // q8 = 4*sb + 2*cc + half
-    const int sb = q8 >> 2, cc = (q8 >> 1) & 1, half = q8 & 1;
-    const int r = 32 * sb + 16 * cc + 8 * (gq >> 1) + 4 * half + (sl >> 2);
+  for (int part = 0; part < 2; ++part) {
+    const int r = 8 * (gq >> 1) + 4 * part + (sl >> 2);
     const int d0 = 16 * (gq & 1) + 4 * (sl & 3);  // db = 0; db adds 32 dims = 4 chunks
-    v_rd[q8] = TILE_B + r * ROW_B + (((d0 >> 3) ^ v_swz(r)) * 16) + (d0 & 7) * 2;
+    v_rd[part] = TILE_B + r * ROW_B + (((d0 >> 3) ^ v_swz(r)) * 16) + (d0 & 7) * 2;
   }
+  // causal triangle of a diagonal half: score i of this lane is key offset
+  // kk(i) within the half, visible iff kk(i) <= tri
+  const int tri = lr - 8 * hh;
 
-  const int last_row = min(p0 + rows_pb, a.S) - 1;
-  const int n_tiles = last_row / BN + 1;
-
-  f32x16 o[RB][DB];
+  f32x16 o[2][2];
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+  for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int i = 0; i < 16; ++i) o[rb][db][i] = 0.f;
-  float m[RB], l[RB];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) { m[rb] = kNegBig; l[rb] = 0.f; }
+  float m[2] = {kNegBig, kNegBig}, l[2] = {0.f, 0.f};
   const float sl2 = a.scale_log2;
-  f32x16 s[RB][2];
-  v8 pbuf[RB][4];
+  f32x16 sA[2], sB[2];   // scores of the current / next half
+  v8 pA[2][2], pB[2][2]; // bf16 P^T of half 0 / half 1 of a tile
 
-  // S^T = K Q^T for one tile (both row blocks; every K operand feeds RB MFMAs)
-  auto qk = [&](const unsigned char* sp) {
-    v8 ka[2][DC];
+  // S^T for one half (K rows 32h..32h+31 of the tile in ring slot `sp`);
+  // RB0: row block 0 takes part
+  auto qk = [&](const unsigned char* sp, int h, f32x16 (&s)[2], auto rb0_c) {
+    constexpr bool RB0 = decltype(rb0_c)::value;
+    v8 ka[DC];
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
+    for (int c = 0; c < DC; ++c)
+      ka[c] = __builtin_bit_cast(v8, *reinterpret_cast<const u32x4*>(sp + k_rd[c] + h * 32 * ROW_B));
 #pragma unroll
-      for (int c = 0; c < DC; ++c)
-        ka[sb][c] = __builtin_bit_cast(
-            v8, *reinterpret_cast<const u32x4*>(sp + k_rd[c] + sb * 32 * ROW_B));
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
+      for (int i = 0; i < 16; ++i) s[rb][i] = 0.f;
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) s[rb][sb][i] = 0.f;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-      for (int c = 0; c < DC; ++c)
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) s[rb][sb] = MM::mma(ka[sb][c], qreg[rb][c], s[rb][sb]);
+    for (int c = 0; c < DC; ++c) {
+      if constexpr (RB0) s[0] = MM::mma(ka[c], qreg[0][c], s[0]);
+      s[1] = MM::mma(ka[c], qreg[1][c], s[1]);
+    }
   };
-  // O^T += V^T P^T for one tile (every V operand feeds RB MFMAs)
-  auto pv = [&](const unsigned char* sp) {
+  // O^T += V^T P^T for one half (V rows 32h..32h+31 of the tile in slot `sp`)
+  auto pv = [&](const unsigned char* sp, int h, const v8 (&p)[2][2], auto rb0_c) {
+    constexpr bool RB0 = decltype(rb0_c)::value;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4)
+    for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-      for (int db = 0; db < DB; ++db) {
-        const uint2 lo = lds_read_tr(sp + v_rd[2 * q4] + db * 64);
-        const uint2 hi = lds_read_tr(sp + v_rd[2 * q4 + 1] + db * 64);
+      for (int db = 0; db < 2; ++db) {
+        const int off = (32 * h + 16 * cc) * ROW_B + db * 64;
+        const uint2 lo = lds_read_tr(sp + v_rd[0] + off);
+        const uint2 hi = lds_read_tr(sp + v_rd[1] + off);
         const v8 vv = __builtin_bit_cast(v8, u32x4{lo.x, lo.y, hi.x, hi.y});
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) o[rb][db] = MM::mma(vv, pbuf[rb][q4], o[rb][db]);
+        if constexpr (RB0) o[0][db] = MM::mma(vv, p[0][cc], o[0][db]);
+        o[1][db] = MM::mma(vv, p[1][cc], o[1][db]);
       }
   };
-  // online softmax of one tile's scores: s -> pbuf, running m / l, O rescale
-  auto softmax = [&](int kpos) {
+  // Online softmax of one half.  Row block rb takes part iff USE0 (rb 0) /
+  // always (rb 1); MASKrb applies the causal triangle.  The running max and
+  // sum are updated without branches (alpha = 1 when the max stays), so the
+  // whole half is one scheduling region with its MFMAs; the returned flag says
+  // whether O must be rescaled once those MFMAs are done.
+  float alpha[2] = {1.f, 1.f};
+  auto smax = [&](f32x16 (&s)[2], v8 (&p)[2][2], auto use0_c, auto mask0_c, auto mask1_c) {
+    constexpr bool USE0 = decltype(use0_c)::value;
+    constexpr bool MASK[2] = {decltype(mask0_c)::value, decltype(mask1_c)::value};
+    float mx[2] = {kNegBig, kNegBig};
 #pragma unroll
-    for (int rb = 0; rb < RB; ++rb) {
-      const int r0 = qpos0 + 32 * rb;
-      if (kpos + BN - 1 > r0) {  // diagonal tile for this row block
-        const int rel = r0 + lr - kpos - 8 * hh;  // visible iff key offset <= rel
+    for (int rb = 0; rb < 2; ++rb) {
+      if (rb == 0 && !USE0) continue;
+      if (MASK[rb]) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kk = 16 * (i >> 3) + (i & 7);
-          if (kk > rel) s[rb][0][i] = -INFINITY;
-          if (kk + 32 > rel) s[rb][1][i] = -INFINITY;
-        }
+        for (int i = 0; i < 16; ++i)
+          if (16 * (i >> 3) + (i & 7) > tri) s[rb][i] = -INFINITY;
       }
-      float mx = fmaxf(s[rb][0][0], s[rb][0][1]);
+      float x = fmaxf(s[rb][0], s[rb][1]);
 #pragma unroll
-      for (int i = 2; i < 16; i += 2) mx = fmaxf(mx, fmaxf(s[rb][0][i], s[rb][0][i + 1]));
+      for (int i = 2; i < 16; i += 2) x = fmaxf(x, fmaxf(s[rb][i], s[rb][i + 1]));
+      auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+      mx[rb] = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl2;
+    }
+    const bool up = (USE0 && mx[0] > m[0] + kRescaleThreshold) || mx[1] > m[1] + kRescaleThreshold;
+    const bool resc = __builtin_amdgcn_ballot_w64(up) != 0;
 #pragma unroll
-      for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(s[rb][1][i], s[rb][1][i + 1]));
-      {
-        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
-        mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl2;
-      }
-      if (__builtin_amdgcn_ballot_w64(mx > m[rb] + kRescaleThreshold) != 0) {
-        const float m_new = fmaxf(m[rb], mx);
-        const float alpha = fast_exp2(m[rb] - m_new);
-        m[rb] = m_new;
-        l[rb] *= alpha;
-#pragma unroll
-        for (int db = 0; db < DB; ++db)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) o[rb][db][i] *= alpha;
-      }
-      const float mr = m[rb];
+    for (int rb = 0; rb < 2; ++rb) {
+      if (rb == 0 && !USE0) continue;
+      const float m_new = resc ? fmaxf(m[rb], mx[rb]) : m[rb];
+      alpha[rb] = fast_exp2(m[rb] - m_new);
+      m[rb] = m_new;
+      const float mr = m_new;
       float ls0 = 0.f, ls1 = 0.f;
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
-        uint32_t w0[4], w1[4];
+        uint32_t wd[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-          const float a0 = fast_exp2(fmaf(s[rb][0][8 * cc + 2 * t], sl2, -mr));
-          const float a1 = fast_exp2(fmaf(s[rb][0][8 * cc + 2 * t + 1], sl2, -mr));
-          const float b0 = fast_exp2(fmaf(s[rb][1][8 * cc + 2 * t], sl2, -mr));
-          const float b1 = fast_exp2(fmaf(s[rb][1][8 * cc + 2 * t + 1], sl2, -mr));
-          ls0 += a0 + a1;
-          ls1 += b0 + b1;
-          w0[t] = MM::pack2(a0, a1);
-          w1[t] = MM::pack2(b0, b1);
+          const float e0 = fast_exp2(fmaf(s[rb][8 * cc + 2 * t], sl2, -mr));
+          const float e1 = fast_exp2(fmaf(s[rb][8 * cc + 2 * t + 1], sl2, -mr));
+          if (t & 1) ls1 += e0 + e1; else ls0 += e0 + e1;
+          wd[t] = MM::pack2(e0, e1);
         }
-        pbuf[rb][cc] = __builtin_bit_cast(v8, u32x4{w0[0], w0[1], w0[2], w0[3]});
-        pbuf[rb][2 + cc] = __builtin_bit_cast(v8, u32x4{w1[0], w1[1], w1[2], w1[3]});
+        p[rb][cc] = __builtin_bit_cast(v8, u32x4{wd[0], wd[1], wd[2], wd[3]});
       }
-      l[rb] += ls0 + ls1;
+      l[rb] = fmaf(l[rb], alpha[rb], ls0 + ls1);
+      // keep this half's softmax inside its slot: without a use here the
+      // compiler sinks it past the tile barrier into the next slot
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+        __asm__ volatile("" ::"v"(__builtin_bit_cast(u32x4, p[rb][cc])));
+      __asm__ volatile("" ::"v"(l[rb]), "v"(m[rb]));
+    }
+    return resc;
+  };
+  auto rescale_o = [&](auto use0_c) {
+    constexpr bool USE0 = decltype(use0_c)::value;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      if (rb == 0 && !USE0) continue;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[rb][db][i] *= alpha[rb];
+    }
+  };
+  // wait until at most `keep` tiles' copies of this wave are in flight
+  auto wait_tiles = [&](int keep) {
+    if (keep >= 2) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * NI) : "memory");
+    else if (keep == 1) __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NI) : "memory");
+    else dma_wait_all();
+  };
+  using TT = std::true_type;
+  using FF = std::false_type;
+  // slot A(t): softmax(t.h0) | PV(t-1.h1), QK(t.h1).  HAS_PV: t > 0;
+  // DIAG: t is the wave's diagonal tile (its second half is hidden from rb 0).
+  auto slot_a = [&](const unsigned char* cur, const unsigned char* prv, auto has_pv_c, auto diag_c) {
+    constexpr bool HAS_PV = decltype(has_pv_c)::value, DIAG = decltype(diag_c)::value;
+    if constexpr (HAS_PV) pv(prv, 1, pB, TT{});
+    qk(cur, 1, sB, std::integral_constant<bool, !DIAG>{});
+    const bool resc = smax(sA, pA, TT{}, std::integral_constant<bool, DIAG>{}, FF{});
+    if (resc) rescale_o(TT{});
+  };
+  // slot B(t): softmax(t.h1) | PV(t.h0), QK(t+1.h0); on the diagonal tile,
+  // rb 1 only, followed by the drain PV(t.h1).
+  auto slot_b = [&](const unsigned char* cur, const unsigned char* nxt, auto diag_c) {
+    constexpr bool DIAG = decltype(diag_c)::value;
+    pv(cur, 0, pA, TT{});
+    if constexpr (!DIAG) {
+      qk(nxt, 0, sA, TT{});
+      if (smax(sB, pB, TT{}, FF{}, FF{})) rescale_o(TT{});
+    } else {
+      if (smax(sB, pB, FF{}, FF{}, TT{})) rescale_o(FF{});
+      pv(cur, 1, pB, FF{});
     }
   };
 
-  // Phase schedule (one barrier after each phase):
-  //   phase 2t   : copy tile t+1 | A: PV(t-1), QK(t) | B: softmax(t-1)
-  //   phase 2t+1 :                 A: softmax(t)     | B: PV(t-1), QK(t)
-  //   phase 2n   : A: PV(n-1) | B: softmax(n-1);  phase 2n+1: B: PV(n-1)
-  // A tile is live for a wave iff it holds a key visible to one of its rows.
-  issue(0, 0);
-  dma_wait_all();
-  block_sync_lds();
-  const int last_q = qpos0 + 32 * RB - 1;
-  bool live_prev = false;
-  int slot = 0, slot_prev = 0;
-  for (int t = 0; t < n_tiles; ++t) {
-    const bool live = wave_active && t * BN <= last_q;
-    const int slot_next = slot == kPpSlots - 1 ? 0 : slot + 1;
-    if (t + 1 < n_tiles) issue(t + 1, slot_next);
-    const unsigned char* cur = lds + slot * SLOT_B;
-    const unsigned char* prev = lds + slot_prev * SLOT_B;
-    if (grp == 0) {
-      __builtin_amdgcn_s_setprio(1);
-      if (live_prev) pv(prev);
-      if (live) qk(cur);
-      __builtin_amdgcn_s_setprio(0);
-    } else if (live_prev) {
-      softmax((t - 1) * BN);
-    }
+  // wait for tile t+1, publish it, and start copying tile t+3 into the slot
+  // that tile t-1 (last read in slot A(t)) has released
+  auto sync_tile = [&](int t) {
+    wait_tiles(min(n_tiles - 2 - t, 1));
     block_sync_lds();
-    if (grp == 0) {
-      if (live) softmax(t * BN);
-    } else {
-      __builtin_amdgcn_s_setprio(1);
-      if (live_prev) pv(prev);
-      if (live) qk(cur);
-      __builtin_amdgcn_s_setprio(0);
-    }
-    dma_wait_all();
-    block_sync_lds();
-    live_prev = live;
-    slot_prev = slot;
-    slot = slot_next;
-  }
-  {
-    const unsigned char* prev = lds + slot_prev * SLOT_B;
-    if (grp == 0) {
-      if (live_prev) pv(prev);
-    } else if (live_prev) {
-      softmax((n_tiles - 1) * BN);
-    }
-    block_sync_lds();
-    if (grp == 1 && live_prev) pv(prev);
-  }
+    if (t + 3 < n_tiles) issue(t + 3);
+  };
+  auto buf = [&](int t) { return lds + (t % kSpBufs) * SLOT_B; };
 
-  if (!wave_active) return;
+  // ---- prologue: tiles 0..2 in flight, wait for tile 0, QK(0.h0)
+  issue(0);
+  if (n_tiles > 1) issue(1);
+  if (n_tiles > 2) issue(2);
+  wait_tiles(min(n_tiles - 1, 2));
+  block_sync_lds();
+  int t = 0;
+  if (n_tw > 0) {
+    qk(lds, 0, sA, TT{});
+    if (n_tw == 1) {
+      slot_a(buf(0), buf(0), FF{}, TT{});
+      sync_tile(0);
+      slot_b(buf(0), buf(0), TT{});
+    } else {
+      slot_a(buf(0), buf(0), FF{}, FF{});
+      sync_tile(0);
+      slot_b(buf(0), buf(1), FF{});
+      for (t = 1; t < n_tw - 1; ++t) {   // steady state
+        slot_a(buf(t), buf(t - 1), TT{}, FF{});
+        sync_tile(t);
+        slot_b(buf(t), buf(t + 1), FF{});
+      }
+      slot_a(buf(t), buf(t - 1), TT{}, TT{});  // diagonal tile
+      sync_tile(t);
+      slot_b(buf(t), buf(t), TT{});
+    }
+    t = n_tw;
+  }
+  for (; t < n_tiles; ++t) sync_tile(t);   // the block's remaining tiles
+
+  if (n_tw == 0) return;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
+  for (int rb = 0; rb < 2; ++rb) {
     float lt = l[rb];
     {  // both lane halves hold partial sums of the same row
       auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lt), __float_as_uint(lt), false, false);
       lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
-    const int qrow = qpos0 + 32 * rb + lr;
+    const int qrow = r0 + 32 * rb + lr;
     if (qrow >= a.S) continue;
     const float inv = 1.0f / lt;
     T* op = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_sb + (int64_t)head * a.o_sh +
             (int64_t)qrow * a.o_ss;
 #pragma unroll
-    for (int db = 0; db < DB; ++db)
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int d = 32 * db + 8 * q4 + 4 * hh;
@@ -822,12 +845,12 @@ hipError_t launch(const PrefillArgs& a, int nwaves, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <typename T, int D>
-hipError_t launch_pp(const PrefillArgs& a, hipStream_t stream) {
+template <typename T>
+hipError_t launch_sp(const PrefillArgs& a, hipStream_t stream) {
   const int n_pairs = a.B * a.Hkv * a.head_chunks;
   dim3 grid((unsigned)(n_pairs * a.n_pb));
-  const size_t smem = (size_t)kPpSlots * 2 * 64 * D * sizeof(T);  // ring of (K + V) tiles
-  hipLaunchKernelGGL((prefill_pp_kernel<T, D>), grid, dim3(512), smem, stream, a);
+  const size_t smem = (size_t)kSpBufs * 2 * 64 * 64 * sizeof(T);  // ring of (K + V) tiles
+  hipLaunchKernelGGL((prefill_sp_kernel<T>), grid, dim3(256), smem, stream, a);
   return hipGetLastError();
 }
 
@@ -908,10 +931,10 @@ extern "C" int32_t mi_attn_prefill(const void* q, const void* k, const void* v,
   a.heads_per_block = gh;
   a.head_chunks = G / gh;
   a.pj = pj;
-  // D = 64 (16-bit): ping-pong kernel, two groups of 4 waves, 64 rows per
-  // wave; D = 128: one group of 4 waves, 32 rows per wave.
-  const bool pp = head_dim == 64 && dtype != MI_DTYPE_F32;
-  const int rows_per_block = pp ? 2 * 64 * pj : 32 * prefill_row_blocks<128>() * pj;
+  // D = 64 (16-bit): software-pipelined kernel, 4 waves of 64 rows; D = 128:
+  // 4 waves of 32 rows.
+  const bool sp = head_dim == 64 && dtype != MI_DTYPE_F32;
+  const int rows_per_block = sp ? 64 * pj : 32 * prefill_row_blocks<128>() * pj;
   a.n_pb = (int32_t)((seq_len + rows_per_block - 1) / rows_per_block);
   a.scale_log2 = sm_scale * kLog2e;
   const int nwaves = gh * pj;
@@ -931,9 +954,9 @@ extern "C" int32_t mi_attn_prefill(const void* q, const void* k, const void* v,
       hipLaunchKernelGGL(prefill_f32_kernel<128>, dim3((unsigned)nblk), dim3(256), 0, st, a);
     e = hipGetLastError();
   } else if (dtype == MI_DTYPE_BF16)
-    e = pp ? launch_pp<bf16_t, 64>(a, st) : launch<bf16_t, 128>(a, nwaves, st);
+    e = sp ? launch_sp<bf16_t>(a, st) : launch<bf16_t, 128>(a, nwaves, st);
   else
-    e = pp ? launch_pp<f16_t, 64>(a, st) : launch<f16_t, 128>(a, nwaves, st);
+    e = sp ? launch_sp<f16_t>(a, st) : launch<f16_t, 128>(a, nwaves, st);
   if (e != hipSuccess) {
     set_last_error("attn_prefill: launch failed: %s", hipGetErrorString(e));
     return (int32_t)e;
