@@ -45,14 +45,16 @@ def _cpu_name() -> str:
     return platform.processor() or "unknown"
 
 
-def _traffic(name: str):
-    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
-    f = ROOT / "profiles" / f"{name}_traffic.json"
-    if f.exists():
-        try:
-            return json.loads(f.read_text()).get("bytes_per_launch")
-        except (ValueError, OSError):
-            return None
+def _traffic(summary: str, key: str):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary under profiles/ (a `key: bytes` line), or None."""
+    f = ROOT / "profiles" / summary
+    try:
+        for ln in f.read_text().splitlines():
+            if ln.startswith(key + ":"):
+                return int(ln.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
     return None
 
 
@@ -78,28 +80,17 @@ def bench_prefill(torch, steps: int, warmup: int) -> dict:
     ev1.record()
     torch.cuda.synchronize()
     ms = ev0.elapsed_time(ev1) / steps
-    # per-launch duration: events around single launches (GPU kept busy by a
-    # queued launch in front so the start event is not taken while idle)
-    durs = []
-    for _ in range(max(3, min(steps, 10))):
-        step()
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record()
-        step()
-        b.record()
-        torch.cuda.synchronize()
-        durs.append(a.elapsed_time(b))
-    durs.sort()
-    kern_ms = durs[len(durs) // 2]
-    achieved = flops / (kern_ms * 1e-3) / 1e12
+    # A step is exactly one kernel launch (prefill_sp_kernel) on torch's current
+    # stream, so the timed region's average is the kernel's average launch
+    # duration (back-to-back launches, no host gaps).
+    achieved = flops / (ms * 1e-3) / 1e12
     return {
         "ms_per_step": ms,
-        "value": flops / (ms * 1e-3) / 1e12,
-        "kernel_ms": kern_ms,
+        "value": achieved,
+        "kernel_ms": ms,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
-                     "traffic": _traffic("prefill_config2")},
+                     "traffic": _traffic("prefill_config2_traffic.md", "hbm_bytes_per_launch")},
         "flops": flops,
     }
 
@@ -156,7 +147,8 @@ def bench_decode_cfg3(torch, steps: int, warmup: int) -> dict:
         "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": ms, "bytes": nbytes,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": _traffic("decode_config3")},
+                     "traffic": _traffic("decode_config3_4_traffic.md",
+                                         "hbm_bytes_per_launch_config3")},
     }
     del graphs, ks, vs
     torch.cuda.empty_cache()
@@ -183,7 +175,9 @@ def bench_decode_cfg4(torch, steps: int, warmup: int) -> dict:
     out = {"config": "4: decode B1 L131072 24/8 D128, splits sweep (combine included)",
            "unit": "GB/s", "by_splits": sweep, "value": best,
            "roofline": {"bound": "hbm", "achieved": best, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(best / HBM_PEAK_GBS, 4), "traffic": None}}
+                        "frac": round(best / HBM_PEAK_GBS, 4),
+                        "traffic": _traffic("decode_config3_4_traffic.md",
+                                            "hbm_bytes_per_launch_config4")}}
     del ks, vs
     torch.cuda.empty_cache()
     return out
