@@ -213,6 +213,53 @@ int32_t mi_w8a16_gemv(const void* x, const int8_t* w, const void* scales,
                       int64_t y_sn, int32_t dtype, int32_t sdtype,
                       void* stream);
 
+/*
+ * Fused decode-step projection (1 <= m <= 16 rows, k % 64 == 0, k <= 16384):
+ *   a   = rmsnorm(x, norm_w, eps) if norm_w != NULL else x   (rounded to dtype)
+ *   y_a = dtype((sum_k a[m,k] * w_a[n,k]) * s_a[n])
+ * then, by epilogue:
+ *   0  y = y_a
+ *   1  y = dtype(res + y_a)                                   (residual add)
+ *   2  y = dtype(dtype(silu(y_a)) * y_b), y_b from w_b / s_b  (SwiGLU, k <= 8192)
+ * Weights int8 [n, k] with 16-byte aligned rows (row strides w_sn_* bytes),
+ * scales in the activation dtype (bf16/fp16), x/res/y rows in elements.  With
+ * norm_w, m*k*2 <= 64 KB.  Each step rounds where the reference's separate ops
+ * round, so results equal the unfused chain up to fp32 summation order.
+ * Replaces, fused into one launch: rmsnorm_triton  src/rms_norm.py:42-77;
+ *   W8A16Linear / w8a16_gemv_launch  src/quant_linear.py:66-120, :250-292;
+ *   the residual adds  src/model.py:113-127; silu(w1 x) * w3 x  src/model.py:23.
+ */
+int32_t mi_w8a16_linear_fused(const void* x, int64_t x_sm, const void* norm_w,
+                              float eps, const int8_t* w_a, const void* s_a,
+                              int64_t w_sn_a, const int8_t* w_b, const void* s_b,
+                              int64_t w_sn_b, const void* res, int64_t res_sm,
+                              void* y, int64_t y_sm, int64_t m, int64_t n,
+                              int64_t k, int32_t epilogue, int32_t dtype,
+                              void* stream);
+
+/*
+ * Fused decode-step attention input (1 <= m <= 16 rows): a = rmsnorm(x) (if
+ * norm_w), q/k/v = W8A16 projections of a (rounded to dtype), then
+ *   q_out[m, h, d]           = RoPE(q)   (q_out [m, n_heads, head_dim])
+ *   cache_k[m, kvh, pos, d]  = RoPE(k),   cache_v[m, kvh, pos, d] = v
+ * with pos = *pos (device int64, shared by all rows; slots outside
+ * [0, capacity) are not written) and RoPE rows cos/sin[pos - rope_row0]
+ * (rope_rows rows, row stride c_ss), rotate-half in fp32 with products and
+ * sum rounded separately.  Cache views are the layer's [m, kvh, T, head_dim]
+ * with element strides (c_sb, c_sh, c_st, 1).
+ * Replaces, fused into one launch: rmsnorm_triton  src/rms_norm.py:42-77;
+ *   wq / wk / wv  src/model_quantized.py:57-60; apply_rotary  src/rope.py:94-119;
+ *   rope_and_cache_update (scatter path)  src/rope.py:188-252, :255-313.
+ */
+int32_t mi_w8a16_qkv_rope_append(
+    const void* x, int64_t x_sm, const void* norm_w, float eps, const int8_t* wq,
+    const void* sq, int64_t wq_sn, const int8_t* wk, const void* sk, int64_t wk_sn,
+    const int8_t* wv, const void* sv, int64_t wv_sn, const void* cos, const void* sin,
+    int64_t c_ss, int64_t rope_row0, int64_t rope_rows, const int64_t* pos, void* q_out,
+    void* cache_k, void* cache_v, int64_t c_sb, int64_t c_sh, int64_t c_st,
+    int64_t capacity, int64_t m, int64_t k, int64_t n_heads, int64_t n_kv_heads,
+    int64_t head_dim, int32_t dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

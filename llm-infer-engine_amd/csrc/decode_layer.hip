@@ -1,0 +1,478 @@
+// Fused W8A16 kernels of one decode step (M <= 16 token rows).
+//
+// A decode step of the W8A16 Llama block (src/model_quantized.py:42-93 with
+// src/model.py:39-127) is a chain of small matrix-vector products; run one
+// launch per reference op, the step is dominated by launch gaps and by
+// kernels too small to reach HBM bandwidth.  These kernels fold every
+// elementwise neighbour of a projection into it:
+//
+//   rmsnorm -> wq | wk | wv -> RoPE(q), RoPE(k) + KV-cache append, v append
+//   wo -> + residual
+//   rmsnorm -> w1 | w3 -> silu(w1 x) * (w3 x)
+//   w2 -> + residual
+//
+// Arithmetic follows the reference op by op: RMSNorm in fp32 rounded once to
+// the activation dtype (src/rms_norm.py:32-38); each projection accumulates
+// x.f32 * q.f32 in fp32 and applies the row scale after the sum
+// (src/quant_linear.py:37-57), rounded to the activation dtype; RoPE,
+// residual adds and silu/mul then act on those rounded values exactly as the
+// reference's separate ops do (src/rope.py:85-86, src/model.py:23, :113-127).
+//
+// GEMV design (MI355X): the int8 weights are the only large operand and are
+// read once.  A workgroup owns a tile of RPB (8 or 16) output rows of one (or,
+// for SwiGLU, two) weight matrices; its NW waves split K.  The products run on
+// v_mfma_f32_16x16x32_{bf16,f16}: the A operand is 16 weight rows x 32 k
+// (int8 converted exactly in registers), the B operand is x^T with the
+// columns beyond M zero.  Each lane loads 16 contiguous int8 of one row; a
+// wave issues every weight load of its K slice before its first MFMA, so the
+// whole matrix is in flight at once (these GEMVs are latency-bound: a few MB
+// each).  With the RMSNorm prologue the normalised rows are staged in LDS and
+// the B operands are read from there; otherwise straight from global memory.
+#include <math.h>
+
+#include "common.hpp"
+
+namespace mi {
+
+enum : int32_t {
+  kEpiStore = 0,     // y = round(acc * s)
+  kEpiResidual = 1,  // y = round(res + round(acc * s))
+  kEpiSwiglu = 2,    // y = round(round(silu(a)) * b), a/b = rounded w1/w3 outputs
+  kEpiQkvRope = 3,   // q -> RoPE -> q_out; k -> RoPE -> cache_k[pos]; v -> cache_v[pos]
+};
+
+struct LayerGemvArgs {
+  const void* x;        // [M, K], unit k stride, row stride x_sm
+  const void* norm_w;   // [K] RMSNorm weight (prologue) or null
+  float eps;
+  const int8_t* w0;     // first matrix [N0, K] (QKV: wq; SwiGLU: w1)
+  const int8_t* w1;     // second matrix (QKV: wk; SwiGLU: w3) or null
+  const int8_t* w2;     // third matrix (QKV: wv) or null
+  const void* s0;       // row scales of w0 / w1 / w2
+  const void* s1;
+  const void* s2;
+  int64_t w_sn0, w_sn1, w_sn2;  // weight row strides (bytes)
+  void* y;              // output [M, N] (store / residual / swiglu) or q_out
+  const void* res;      // residual [M, N]
+  int64_t x_sm, y_sm, res_sm;
+  int32_t M, K, N;      // N: output rows (QKV: Hq*D)
+  int32_t n_tiles0;     // QKV: tiles of wq (the rest are wk then wv)
+  int32_t n_tiles1;
+  // QKV + RoPE + append
+  const void* cos;      // [rows, D/2] tables, row stride c_ss (elements); position
+  const void* sin;      //   p uses row p - rope_row0
+  int64_t c_ss, rope_row0, rope_rows;
+  const int64_t* pos;   // device position (one for all rows)
+  void* ck;             // cache views of this layer: element (m, h, p, d) at
+  void* cv;             //   m*c_sb + h*c_sh + p*c_st + d
+  int64_t c_sb, c_sh, c_st;
+  int64_t capacity;     // T
+  int32_t Hq, Hkv, D;
+};
+
+template <typename T> struct LMfma;
+template <> struct LMfma<bf16_t> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  __device__ static inline f32x4 mma(const v8& a, const v8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct LMfma<f16_t> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  __device__ static inline f32x4 mma(const v8& a, const v8& b, const f32x4& c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// 8 signed bytes (two words) -> 8 activation-dtype values (exact).
+template <typename T, typename V8>
+__device__ inline V8 i8x8_cvt(uint32_t lo, uint32_t hi) {
+  V8 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    r[i] = (T)(float)(int8_t)(lo >> (8 * i));
+    r[4 + i] = (T)(float)(int8_t)(hi >> (8 * i));
+  }
+  return r;
+}
+
+__device__ inline float silu_f32(float a) { return a / (1.0f + expf(-a)); }
+
+// Weight row of tile row r (0..15) for tile `tile`: rows 0..RPB-1 of the tile;
+// for the RoPE epilogue a tile holds 8 rotation pairs: rows i and i+8 are head
+// dims d and d + D/2.
+template <int EPI>
+__device__ inline int tile_row(int tile_in_mat, int r, int D) {
+  if constexpr (EPI == kEpiQkvRope) {
+    const int half = D >> 1, tiles_per_head = half >> 3;
+    const int head = tile_in_mat / tiles_per_head, j = tile_in_mat % tiles_per_head;
+    return head * D + 8 * j + (r & 7) + ((r >> 3) ? half : 0);
+  } else {
+    return tile_in_mat * 16 + r;
+  }
+}
+
+template <typename T, int NW, int MAXC, bool NORM, int EPI>
+__global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
+  using MM = LMfma<T>;
+  typedef typename MM::v8 v8;
+  constexpr int NMAT = EPI == kEpiSwiglu ? 2 : 1;      // A streams per tile
+  // MAXC: 64-k chunks per wave (NW * MAXC covers K)
+  extern __shared__ __align__(16) unsigned char smem[];
+  T* xs = reinterpret_cast<T*>(smem);                   // NORM: [M][K] normalised x
+  f32x4* red = reinterpret_cast<f32x4*>(smem + (NORM ? (size_t)a.M * a.K * sizeof(T) : 0));
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;    // A: weight row in tile / k group
+  const int m = lane & 15;                   // B: x row
+  const bool m_ok = m < a.M;
+
+  // ---- which matrix / tile this block owns
+  int tile = blockIdx.x;
+  int mat = 0;
+  if constexpr (EPI == kEpiQkvRope) {
+    if (tile >= a.n_tiles0) {
+      tile -= a.n_tiles0;
+      mat = 1;
+      if (tile >= a.n_tiles1) { tile -= a.n_tiles1; mat = 2; }
+    }
+  }
+  const int8_t* wm = mat == 0 ? a.w0 : (mat == 1 ? a.w1 : a.w2);
+  const int64_t w_sn = mat == 0 ? a.w_sn0 : (mat == 1 ? a.w_sn1 : a.w_sn2);
+  const int n_in_mat = tile_row<EPI>(tile, r, a.D);     // this lane's weight row
+  const int n_valid = EPI == kEpiQkvRope ? (mat == 0 ? a.Hq : a.Hkv) * a.D : a.N;
+  const bool row_ok = n_in_mat < n_valid;
+  const int8_t* wrow0 = wm + (int64_t)(row_ok ? n_in_mat : 0) * w_sn;
+  const int8_t* wrow1 = NMAT == 2 ? a.w1 + (int64_t)(row_ok ? n_in_mat : 0) * a.w_sn1 : nullptr;
+
+  // ---- issue every weight load of this wave's K slice
+  const int n_chunks = a.K >> 6;                        // K % 64 == 0 (host-checked)
+  const int cpw = (n_chunks + NW - 1) / NW;
+  const int c_lo = w * cpw, c_hi = min(c_lo + cpw, n_chunks);
+  u32x4 wq[NMAT][MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = c_lo + i;
+    const bool ok = c < c_hi && row_ok;
+    const int k0 = c * 64 + 16 * g;
+    wq[0][i] = ok ? load16_stream(wrow0 + k0) : u32x4{0, 0, 0, 0};
+    if constexpr (NMAT == 2) wq[1][i] = ok ? load16_stream(wrow1 + k0) : u32x4{0, 0, 0, 0};
+  }
+
+  // ---- RMSNorm prologue: normalised rows into LDS (overlaps the loads above)
+  if constexpr (NORM) {
+    const T* nw = reinterpret_cast<const T*>(a.norm_w);
+    for (int row = w; row < a.M; row += NW) {
+      const T* xr = reinterpret_cast<const T*>(a.x) + (int64_t)row * a.x_sm;
+      float ss = 0.f;
+      for (int k = lane * 8; k < a.K; k += 512) {
+        float v[8];
+        Chunk<T>::unpack(load16(xr + k), v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) ss += shfl_xor_f32(ss, off);
+      const float rstd = 1.0f / sqrtf(ss / (float)a.K + a.eps);
+      for (int k = lane * 8; k < a.K; k += 512) {
+        float v[8], wv[8];
+        Chunk<T>::unpack(load16(xr + k), v);
+        Chunk<T>::unpack(load16(nw + k), wv);
+        typedef T t8 __attribute__((ext_vector_type(8)));
+        t8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = Elem<T>::from_f32(v[e] * rstd * wv[e]);
+        *reinterpret_cast<t8*>(xs + (int64_t)row * a.K + k) = o;
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- MFMAs over the slice
+  const T* xg = reinterpret_cast<const T*>(a.x) + (int64_t)(m_ok ? m : 0) * a.x_sm;
+  f32x4 acc[NMAT];
+#pragma unroll
+  for (int t = 0; t < NMAT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = c_lo + i;
+    if (c >= c_hi) break;
+    const int k0 = c * 64 + 16 * g;
+    v8 xb0, xb1;
+    if (m_ok) {
+      const T* xp = NORM ? xs + (int64_t)m * a.K + k0 : xg + k0;
+      xb0 = __builtin_bit_cast(v8, load16(xp));
+      xb1 = __builtin_bit_cast(v8, load16(xp + 8));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { xb0[e] = (T)0.f; xb1[e] = (T)0.f; }
+    }
+#pragma unroll
+    for (int t = 0; t < NMAT; ++t) {
+      acc[t] = MM::mma(i8x8_cvt<T, v8>(wq[t][i].x, wq[t][i].y), xb0, acc[t]);
+      acc[t] = MM::mma(i8x8_cvt<T, v8>(wq[t][i].z, wq[t][i].w), xb1, acc[t]);
+    }
+  }
+
+  // ---- reduce the NW waves' partial sums
+  if (w != 0) {
+#pragma unroll
+    for (int t = 0; t < NMAT; ++t) red[((w - 1) * NMAT + t) * 64 + lane] = acc[t];
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int ww = 1; ww < NW; ++ww)
+#pragma unroll
+    for (int t = 0; t < NMAT; ++t) acc[t] += red[((ww - 1) * NMAT + t) * 64 + lane];
+
+  // acc[t][i] = C[tile row 4*g + i][x row m]
+  auto scale_of = [&](const void* s, int n) {
+    return Elem<T>::to_f32(reinterpret_cast<const T*>(s)[n]);
+  };
+  if constexpr (EPI == kEpiQkvRope) {
+    // rows 4g+i (g < 2) are dims d = 8j + 4g + i, their partners (rows +8) sit
+    // in lane + 32: swap the rounded projections across the lane halves
+    const void* sc = mat == 0 ? a.s0 : (mat == 1 ? a.s1 : a.s2);
+    const int half = a.D >> 1, tph = half >> 3;
+    const int head = tile / tph, j8 = tile % tph;
+    float yv[4], yp[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = 4 * g + i;
+      const int n = head * a.D + 8 * j8 + (rr & 7) + ((rr >> 3) ? half : 0);
+      yv[i] = Elem<T>::to_f32(Elem<T>::from_f32(acc[0][i] * scale_of(sc, n)));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(yv[i]), __float_as_uint(yv[i]),
+                                                 false, false);
+      yp[i] = __uint_as_float(lane < 32 ? sw[1] : sw[0]);
+    }
+    if (!m_ok) return;
+    const int64_t p = *a.pos;
+    const bool hi = g >= 2;                       // rows 8..15: second half of the pair
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ii = 8 * j8 + 4 * (g & 1) + i;    // rotation index, 0 <= ii < half
+      const int d = ii + (hi ? half : 0);
+      T out;
+      if (mat == 2) {
+        out = Elem<T>::from_f32(yv[i]);           // v: appended unrotated (bitwise)
+      } else {
+        // rows outside the table are clamped (callers keep positions in range)
+        const int64_t crow = min(max(p - a.rope_row0, (int64_t)0), a.rope_rows - 1);
+        const float cs = Elem<T>::to_f32(reinterpret_cast<const T*>(a.cos)[crow * a.c_ss + ii]);
+        const float sn = Elem<T>::to_f32(reinterpret_cast<const T*>(a.sin)[crow * a.c_ss + ii]);
+        const float x1 = hi ? yp[i] : yv[i], x2 = hi ? yv[i] : yp[i];
+        T y1, y2;
+        {
+#pragma clang fp contract(off)
+          const float x1c = x1 * cs, x2s = x2 * sn, x2c = x2 * cs, x1s = x1 * sn;
+          y1 = Elem<T>::from_f32(x1c - x2s);
+          y2 = Elem<T>::from_f32(x2c + x1s);
+        }
+        out = hi ? y2 : y1;
+      }
+      if (mat == 0) {
+        reinterpret_cast<T*>(a.y)[((int64_t)m * a.Hq + head) * a.D + d] = out;
+      } else if (p >= 0 && p < a.capacity) {
+        T* c = reinterpret_cast<T*>(mat == 1 ? a.ck : a.cv);
+        c[(int64_t)m * a.c_sb + (int64_t)head * a.c_sh + p * a.c_st + d] = out;
+      }
+    }
+  } else {
+    if (!m_ok) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = tile * 16 + 4 * g + i;
+      if (n >= a.N) continue;
+      float v = Elem<T>::to_f32(Elem<T>::from_f32(acc[0][i] * scale_of(a.s0, n)));
+      if constexpr (EPI == kEpiResidual) {
+        const float rv = Elem<T>::to_f32(reinterpret_cast<const T*>(a.res)[(int64_t)m * a.res_sm + n]);
+        v = Elem<T>::to_f32(Elem<T>::from_f32(rv + v));
+      } else if constexpr (EPI == kEpiSwiglu) {
+        const float b = Elem<T>::to_f32(Elem<T>::from_f32(acc[1][i] * scale_of(a.s1, n)));
+        const float sa = Elem<T>::to_f32(Elem<T>::from_f32(silu_f32(v)));
+        v = sa * b;
+      }
+      reinterpret_cast<T*>(a.y)[(int64_t)m * a.y_sm + n] = Elem<T>::from_f32(v);
+    }
+  }
+}
+
+namespace {
+
+template <typename T, int NW, int MAXC, bool NORM, int EPI>
+hipError_t launch_layer_gemv(const LayerGemvArgs& a, int n_blocks, hipStream_t st) {
+  size_t smem = (size_t)(NW - 1) * (EPI == kEpiSwiglu ? 2 : 1) * 64 * sizeof(f32x4);
+  if (NORM) smem += (size_t)a.M * a.K * sizeof(T);
+  hipLaunchKernelGGL((layer_gemv_kernel<T, NW, MAXC, NORM, EPI>), dim3((unsigned)n_blocks),
+                     dim3(64 * NW), smem, st, a);
+  return hipGetLastError();
+}
+
+// Waves per block and 64-k chunks per wave: each wave's slice of K is loaded
+// in one go (MAXC registers of 16 bytes per lane and matrix).
+template <typename T, bool NORM, int EPI>
+hipError_t dispatch_nw(const LayerGemvArgs& a, int n_blocks, hipStream_t st) {
+  const int chunks = a.K / 64;
+  if (chunks <= 4 * 8) return launch_layer_gemv<T, 4, 8, NORM, EPI>(a, n_blocks, st);
+  if (chunks <= 8 * 8) return launch_layer_gemv<T, 8, 8, NORM, EPI>(a, n_blocks, st);
+  if (EPI == kEpiSwiglu || chunks <= 8 * 16)  // SwiGLU: K <= 8192 (host-checked)
+    return launch_layer_gemv<T, 8, 16, NORM, EPI>(a, n_blocks, st);
+  return launch_layer_gemv<T, 16, 16, NORM, EPI>(a, n_blocks, st);
+}
+
+template <typename T, int EPI>
+hipError_t dispatch_norm(const LayerGemvArgs& a, int n_blocks, hipStream_t st) {
+  return a.norm_w != nullptr ? dispatch_nw<T, true, EPI>(a, n_blocks, st)
+                             : dispatch_nw<T, false, EPI>(a, n_blocks, st);
+}
+
+int32_t check_x(const void* x, int64_t M, int64_t K, int64_t x_sm, const void* norm_w,
+                int32_t dtype, const char* what) {
+  if (x == nullptr) {
+    set_last_error("%s: null x", what);
+    return MI_ERR_INVALID;
+  }
+  if (dtype != MI_DTYPE_BF16 && dtype != MI_DTYPE_F16) {
+    set_last_error("%s: activations must be bf16 or fp16 (dtype %d)", what, (int)dtype);
+    return MI_ERR_UNSUPPORTED;
+  }
+  if (M < 1 || M > 16 || K < 64 || K % 64 != 0 || K > 16 * 16 * 64) {
+    set_last_error("%s: need 1 <= M <= 16 and K a multiple of 64 up to 16384 (M=%lld K=%lld)",
+                   what, (long long)M, (long long)K);
+    return MI_ERR_UNSUPPORTED;
+  }
+  if ((uintptr_t)x % 16 != 0 || (x_sm * 2) % 16 != 0) {
+    set_last_error("%s: x rows must be 16-byte aligned", what);
+    return MI_ERR_INVALID;
+  }
+  if (norm_w != nullptr && ((uintptr_t)norm_w % 16 != 0 || M * K * 2 > 64 * 1024)) {
+    set_last_error("%s: RMSNorm prologue needs a 16-byte aligned weight and M*K*2 <= 64 KB",
+                   what);
+    return MI_ERR_UNSUPPORTED;
+  }
+  return MI_OK;
+}
+
+int32_t check_w(const int8_t* w, const void* s, int64_t w_sn, const char* what) {
+  if (w == nullptr || s == nullptr) {
+    set_last_error("%s: null weight or scales", what);
+    return MI_ERR_INVALID;
+  }
+  if ((uintptr_t)w % 16 != 0 || w_sn % 16 != 0) {
+    set_last_error("%s: weight rows must be 16-byte aligned", what);
+    return MI_ERR_UNSUPPORTED;
+  }
+  return MI_OK;
+}
+
+}  // namespace
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int32_t mi_w8a16_linear_fused(
+    const void* x, int64_t x_sm, const void* norm_w, float eps, const int8_t* w_a,
+    const void* s_a, int64_t w_sn_a, const int8_t* w_b, const void* s_b, int64_t w_sn_b,
+    const void* res, int64_t res_sm, void* y, int64_t y_sm, int64_t M, int64_t N, int64_t K,
+    int32_t epilogue, int32_t dtype, void* stream) {
+  const char* what = "w8a16_linear_fused";
+  int32_t st = check_x(x, M, K, x_sm, norm_w, dtype, what);
+  if (st != MI_OK) return st;
+  if ((st = check_w(w_a, s_a, w_sn_a, what)) != MI_OK) return st;
+  if (y == nullptr || N < 1 || N > INT32_MAX - 16) {
+    set_last_error("%s: null output or bad N (%lld)", what, (long long)N);
+    return MI_ERR_INVALID;
+  }
+  if (epilogue == kEpiResidual && res == nullptr) {
+    set_last_error("%s: residual epilogue needs res", what);
+    return MI_ERR_INVALID;
+  }
+  if (epilogue == kEpiSwiglu && (st = check_w(w_b, s_b, w_sn_b, what)) != MI_OK) return st;
+  if (epilogue == kEpiSwiglu && K > 8192) {
+    set_last_error("%s: SwiGLU epilogue supports K <= 8192 (K=%lld)", what, (long long)K);
+    return MI_ERR_UNSUPPORTED;
+  }
+  if (epilogue != kEpiStore && epilogue != kEpiResidual && epilogue != kEpiSwiglu) {
+    set_last_error("%s: unknown epilogue %d", what, (int)epilogue);
+    return MI_ERR_INVALID;
+  }
+  LayerGemvArgs a{};
+  a.x = x; a.norm_w = norm_w; a.eps = eps;
+  a.w0 = w_a; a.s0 = s_a; a.w_sn0 = w_sn_a;
+  a.w1 = w_b; a.s1 = s_b; a.w_sn1 = w_sn_b;
+  a.y = y; a.res = res; a.x_sm = x_sm; a.y_sm = y_sm; a.res_sm = res_sm;
+  a.M = (int32_t)M; a.K = (int32_t)K; a.N = (int32_t)N;
+  const int n_blocks = (int)((N + 15) / 16);
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e;
+  if (dtype == MI_DTYPE_BF16) {
+    e = epilogue == kEpiStore ? dispatch_norm<bf16_t, kEpiStore>(a, n_blocks, s)
+        : epilogue == kEpiResidual ? dispatch_norm<bf16_t, kEpiResidual>(a, n_blocks, s)
+                                   : dispatch_norm<bf16_t, kEpiSwiglu>(a, n_blocks, s);
+  } else {
+    e = epilogue == kEpiStore ? dispatch_norm<f16_t, kEpiStore>(a, n_blocks, s)
+        : epilogue == kEpiResidual ? dispatch_norm<f16_t, kEpiResidual>(a, n_blocks, s)
+                                   : dispatch_norm<f16_t, kEpiSwiglu>(a, n_blocks, s);
+  }
+  if (e != hipSuccess) {
+    set_last_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return (int32_t)e;
+  }
+  return MI_OK;
+}
+
+extern "C" int32_t mi_w8a16_qkv_rope_append(
+    const void* x, int64_t x_sm, const void* norm_w, float eps, const int8_t* wq,
+    const void* sq, int64_t wq_sn, const int8_t* wk, const void* sk, int64_t wk_sn,
+    const int8_t* wv, const void* sv, int64_t wv_sn, const void* cos, const void* sin,
+    int64_t c_ss, int64_t rope_row0, int64_t rope_rows, const int64_t* pos, void* q_out,
+    void* cache_k, void* cache_v,
+    int64_t c_sb, int64_t c_sh, int64_t c_st, int64_t capacity, int64_t M, int64_t K,
+    int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int32_t dtype, void* stream) {
+  const char* what = "w8a16_qkv_rope_append";
+  int32_t st = check_x(x, M, K, x_sm, norm_w, dtype, what);
+  if (st != MI_OK) return st;
+  if ((st = check_w(wq, sq, wq_sn, what)) != MI_OK) return st;
+  if ((st = check_w(wk, sk, wk_sn, what)) != MI_OK) return st;
+  if ((st = check_w(wv, sv, wv_sn, what)) != MI_OK) return st;
+  if (cos == nullptr || sin == nullptr || pos == nullptr || q_out == nullptr ||
+      cache_k == nullptr || cache_v == nullptr || rope_rows < 1 || c_ss < head_dim / 2) {
+    set_last_error("%s: null rope table, position, output or cache pointer", what);
+    return MI_ERR_INVALID;
+  }
+  if (head_dim < 16 || head_dim % 16 != 0 || n_heads < 1 || n_kv_heads < 1 ||
+      n_heads % n_kv_heads != 0 || capacity < 1 || n_heads * head_dim > INT32_MAX / 2) {
+    set_last_error("%s: unsupported heads (%lld/%lld) or head_dim %lld", what,
+                   (long long)n_heads, (long long)n_kv_heads, (long long)head_dim);
+    return MI_ERR_UNSUPPORTED;
+  }
+  LayerGemvArgs a{};
+  a.x = x; a.norm_w = norm_w; a.eps = eps;
+  a.w0 = wq; a.s0 = sq; a.w_sn0 = wq_sn;
+  a.w1 = wk; a.s1 = sk; a.w_sn1 = wk_sn;
+  a.w2 = wv; a.s2 = sv; a.w_sn2 = wv_sn;
+  a.y = q_out; a.x_sm = x_sm;
+  a.M = (int32_t)M; a.K = (int32_t)K; a.N = (int32_t)(n_heads * head_dim);
+  a.cos = cos; a.sin = sin; a.c_ss = c_ss; a.rope_row0 = rope_row0; a.rope_rows = rope_rows;
+  a.pos = pos;
+  a.ck = cache_k; a.cv = cache_v; a.c_sb = c_sb; a.c_sh = c_sh; a.c_st = c_st;
+  a.capacity = capacity;
+  a.Hq = (int32_t)n_heads; a.Hkv = (int32_t)n_kv_heads; a.D = (int32_t)head_dim;
+  const int tph = (int)(head_dim / 16);   // tiles (8 rotation pairs each) per head
+  a.n_tiles0 = (int32_t)(n_heads * tph);
+  a.n_tiles1 = (int32_t)(n_kv_heads * tph);
+  const int n_blocks = a.n_tiles0 + 2 * a.n_tiles1;
+  hipStream_t s = (hipStream_t)stream;
+  hipError_t e = dtype == MI_DTYPE_BF16 ? dispatch_norm<bf16_t, kEpiQkvRope>(a, n_blocks, s)
+                                        : dispatch_norm<f16_t, kEpiQkvRope>(a, n_blocks, s);
+  if (e != hipSuccess) {
+    set_last_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return (int32_t)e;
+  }
+  return MI_OK;
+}

@@ -109,6 +109,23 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i64, _i64, _i64, _i64, _i64, _i64,    # x_sm x_sk w_sn s_sn y_sm y_sn
         _i32, _i32, _ptr,                      # dtype sdtype stream
     ]),
+    "mi_w8a16_linear_fused": (_i32, [
+        _ptr, _i64, _ptr, _f32,                # x x_sm norm_w eps
+        _ptr, _ptr, _i64,                      # w_a s_a w_sn_a
+        _ptr, _ptr, _i64,                      # w_b s_b w_sn_b
+        _ptr, _i64, _ptr, _i64,                # res res_sm y y_sm
+        _i64, _i64, _i64,                      # M N K
+        _i32, _i32, _ptr,                      # epilogue dtype stream
+    ]),
+    "mi_w8a16_qkv_rope_append": (_i32, [
+        _ptr, _i64, _ptr, _f32,                # x x_sm norm_w eps
+        _ptr, _ptr, _i64, _ptr, _ptr, _i64, _ptr, _ptr, _i64,   # wq sq wk sk wv sv (+ row strides)
+        _ptr, _ptr, _i64, _i64, _i64,          # cos sin c_ss rope_row0 rope_rows
+        _ptr, _ptr, _ptr, _ptr,                # pos q_out cache_k cache_v
+        _i64, _i64, _i64, _i64,                # c_sb c_sh c_st capacity
+        _i64, _i64, _i64, _i64, _i64,          # M K n_heads n_kv_heads head_dim
+        _i32, _ptr,                            # dtype stream
+    ]),
 }
 
 _lock = threading.Lock()

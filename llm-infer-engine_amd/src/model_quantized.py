@@ -5,12 +5,19 @@ projections; embedding, norms and lm_head stay in the activation dtype
 (src/model_quantized.py:137-142).  ``build_random_quantized`` makes the seeded
 random-init model of the W8A16 decode benchmark: bf16 master weights drawn on
 the device, quantised with quantize_weight_symmetric_per_channel.
+
+Single-token decode (query length 1, up to 16 rows) runs each block through
+the fused decode-layer kernels (src/decode_layer.py): five launches per layer
+with the same rounding points as the op-by-op composition, which remains the
+path for prefill and for shapes the fused kernels do not take.
 """
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
 
+from . import decode_layer
+from .flash_decode import flash_decode
 from .model import Attention, FeedForward, Llama3, TransformerBlock
 from .quant_linear import W8A16Linear
 from .quant_utils import quantize_weight_symmetric_per_channel
@@ -27,8 +34,62 @@ class QuantizedAttention(Attention):
 
 
 class QuantizedTransformerBlock(TransformerBlock):
+    #: run single-token decode through the fused decode-layer kernels
+    fused_decode = True
+
     def __init__(self, args, linear=W8A16Linear):
         super().__init__(args, W8A16Linear)
+
+    def _fusable(self, x, rope_cos, kv_cache, layer_idx, positions, rope_by_position) -> bool:
+        if not self.fused_decode or kv_cache is None or layer_idx is None or x.shape[1] != 1:
+            return False
+        if positions is not None and not rope_by_position:
+            return False  # per-step sliced tables at a device position: op chain
+        attn, ff = self.attention, self.feed_forward
+        B, _, dim = x.shape
+        if (B > kv_cache.max_batch_size or kv_cache.k.dtype != x.dtype
+                or rope_cos.dtype != x.dtype or attn.head_dim % 16 != 0 or not x.is_contiguous()):
+            return False
+        dt, sup = x.dtype, decode_layer.supported
+        n_o = attn.n_heads * attn.head_dim
+        return (decode_layer.aligned(x.view(B, dim))
+                and sup(B, dim, dt, attn.wq, self.attention_norm.weight)
+                and sup(B, dim, dt, attn.wk) and sup(B, dim, dt, attn.wv)
+                and sup(B, n_o, dt, attn.wo)
+                and sup(B, dim, dt, ff.w1, self.ffn_norm.weight) and sup(B, dim, dt, ff.w3)
+                and sup(B, ff.w1.out_features, dt, ff.w2))
+
+    def forward(self, x, rope_cos, rope_sin, layer_idx=None, start_pos=0, kv_cache=None,
+                use_cuda_graph=False, scatter_positions=None, decode_attn_mask=None, **ext):
+        positions = scatter_positions if (use_cuda_graph and scatter_positions is not None) else None
+        by_pos = bool(ext.get("rope_by_position", False))
+        if not self._fusable(x, rope_cos, kv_cache, layer_idx, positions, by_pos):
+            return super().forward(x, rope_cos, rope_sin, layer_idx=layer_idx, start_pos=start_pos,
+                                   kv_cache=kv_cache, use_cuda_graph=use_cuda_graph,
+                                   scatter_positions=scatter_positions,
+                                   decode_attn_mask=decode_attn_mask, **ext)
+        attn, ff = self.attention, self.feed_forward
+        B, _, dim = x.shape
+        x2 = x.view(B, dim)
+        if positions is not None:  # graph path: device position, full-table RoPE rows
+            pos, row0 = positions, 0
+            if pos.dtype != torch.int64:
+                pos = pos.to(torch.int64)
+        else:
+            pos = torch.full((1,), int(start_pos), dtype=torch.int64, device=x.device)
+            row0 = 0 if by_pos else int(start_pos)
+        q = decode_layer.qkv_rope_append(x2, attn, self.attention_norm.weight,
+                                         self.attention_norm.eps, rope_cos, rope_sin, row0, pos,
+                                         kv_cache, layer_idx)
+        ck, cv = kv_cache.k[layer_idx, :B], kv_cache.v[layer_idx, :B]
+        if positions is None:
+            ck, cv = ck[:, :, :int(start_pos) + 1], cv[:, :, :int(start_pos) + 1]
+        o = flash_decode(q, ck, cv, mask=decode_attn_mask, seq_lens=ext.get("seq_lens"))
+        h = decode_layer.linear_fused(o.view(B, -1), attn.wo, residual=x2)
+        g = decode_layer.linear_fused(h, ff.w1, norm_weight=self.ffn_norm.weight,
+                                      eps=self.ffn_norm.eps, lin_b=ff.w3)
+        y = decode_layer.linear_fused(g, ff.w2, residual=h)
+        return y.view(B, 1, dim)
 
 
 class Llama3Quantized(Llama3):

@@ -1,0 +1,173 @@
+"""GPU parity of the fused W8A16 decode-layer kernels (mi_w8a16_linear_fused,
+mi_w8a16_qkv_rope_append) against the CPU oracle's op-by-op composition
+(rmsnorm -> w8a16 -> RoPE / residual / silu*mul) and against the engine's own
+unfused GPU chain.  bf16 outputs within 2e-2 of the output scale (the W8A16
+bar used for the unfused GEMV); the fused and unfused GPU chains differ only in
+fp32 summation order, so they agree to a bf16 rounding step (1e-2 of scale).
+"""
+import pytest
+import torch
+
+from helpers import max_abs, randn
+from oracle import quant as oq
+from oracle import rope as orope
+
+pytestmark = pytest.mark.gpu
+
+
+def _linear(dev, K, N, dtype, seed):
+    from src.quant_linear import W8A16Linear
+    from src.quant_utils import quantize_weight_symmetric_per_channel
+    w = randn((N, K), seed, torch.float32, dev, scale=K ** -0.5)
+    q, s = quantize_weight_symmetric_per_channel(w.to(dtype))
+    lin = W8A16Linear(K, N).to(dev)
+    lin.weight.data = q
+    lin.scales.data = s.to(dtype)
+    return lin
+
+
+def _close(a, b, tol):
+    scale = float(b.float().abs().max()) + 1e-6
+    assert max_abs(a, b) < tol * scale, (max_abs(a, b), scale)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,K,N", [(1, 256, 384), (3, 2048, 512), (8, 2048, 2048), (16, 1024, 256),
+                                   (8, 8192, 2048)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_linear_store_and_residual(dev, dtype, M, K, N, norm):
+    if norm and M * K * 2 > 64 * 1024:
+        pytest.skip("the RMSNorm prologue stages at most 64 KB of rows")
+    from src import decode_layer
+    from src.rms_norm import rmsnorm_triton
+    lin = _linear(dev, K, N, dtype, 1)
+    x = randn((M, K), 2, dtype, dev)
+    nw = (1.0 + 0.1 * randn((K,), 3, torch.float32)).to(dtype).to(dev) if norm else None
+    res = randn((M, N), 4, dtype, dev)
+    y = decode_layer.linear_fused(x, lin, norm_weight=nw, eps=1e-5)
+    yr = decode_layer.linear_fused(x, lin, norm_weight=nw, eps=1e-5, residual=res)
+    a = oq.rmsnorm(x, nw, 1e-5) if norm else x.cpu()
+    ref = oq.w8a16(a, lin.weight, lin.scales)
+    _close(y, ref, 2e-2)
+    _close(yr, (res.cpu().float() + ref.float()).to(dtype), 2e-2)
+    # the unfused GPU chain (RMSNorm kernel, GEMV kernel, torch add)
+    un = lin(rmsnorm_triton(x, nw, 1e-5) if norm else x)
+    _close(y, un, 1e-2)
+    _close(yr, res + un, 1e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", [1, 5, 8])
+def test_swiglu_with_norm(dev, dtype, M):
+    from src import decode_layer
+    from src.rms_norm import rmsnorm_triton
+    K, N = 2048, 1024
+    w1, w3 = _linear(dev, K, N, dtype, 5), _linear(dev, K, N, dtype, 6)
+    x = randn((M, K), 7, dtype, dev, scale=3.0)
+    nw = (1.0 + 0.1 * randn((K,), 8, torch.float32)).to(dtype).to(dev)
+    y = decode_layer.linear_fused(x, w1, norm_weight=nw, eps=1e-5, lin_b=w3)
+    a = oq.rmsnorm(x, nw, 1e-5)
+    g = oq.w8a16(a, w1.weight, w1.scales).float()
+    ref = ((g * torch.sigmoid(g)).to(dtype).float() * oq.w8a16(a, w3.weight, w3.scales).float()).to(dtype)
+    _close(y, ref, 2e-2)
+    xn = rmsnorm_triton(x, nw, 1e-5)
+    _close(y, torch.nn.functional.silu(w1(xn)) * w3(xn), 1e-2)
+
+
+class _Attn:
+    def __init__(self, dev, dim, Hq, Hkv, D, dtype):
+        self.n_heads, self.n_kv_heads, self.head_dim = Hq, Hkv, D
+        self.wq = _linear(dev, dim, Hq * D, dtype, 11)
+        self.wk = _linear(dev, dim, Hkv * D, dtype, 12)
+        self.wv = _linear(dev, dim, Hkv * D, dtype, 13)
+
+
+class _Cache:
+    def __init__(self, dev, L, MB, Hkv, T, D, dtype):
+        self.k = randn((L, MB, Hkv, T, D), 21, dtype, dev)
+        self.v = randn((L, MB, Hkv, T, D), 22, dtype, dev)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,Hq,Hkv,D", [(8, 32, 8, 64), (3, 24, 8, 128), (1, 4, 1, 64), (16, 8, 2, 32)])
+@pytest.mark.parametrize("by_position", [True, False])
+def test_qkv_rope_append(dev, dtype, M, Hq, Hkv, D, by_position):
+    from src import decode_layer
+    from src.rope import DeviceRopeTable, apply_rotary
+    dim, T, L, layer, p = 512, 128, 2, 1, 77
+    attn = _Attn(dev, dim, Hq, Hkv, D, dtype)
+    cache = _Cache(dev, L, M + 1, Hkv, T, D, dtype)
+    k0, v0 = cache.k.clone(), cache.v.clone()
+    x = randn((M, dim), 31, dtype, dev)
+    nw = (1.0 + 0.1 * randn((dim,), 32, torch.float32)).to(dtype).to(dev)
+    fc = orope.freqs_cis(D, T, 500000.0)
+    table = DeviceRopeTable(fc, dtype, dev)
+    cos, sin = (table.cos, table.sin) if by_position else table.rows(p, 1)
+    row0 = 0 if by_position else p
+    pos = torch.full((1,), p, dtype=torch.int64, device=dev)
+    q = decode_layer.qkv_rope_append(x, attn, nw, 1e-5, cos, sin, row0, pos, cache, layer)
+    # oracle: rmsnorm -> projections (rounded) -> rotate-half at row p
+    a = oq.rmsnorm(x, nw, 1e-5)
+    oc, os_ = orope.cos_sin(fc[p:p + 1], dtype)
+    rq = orope.rotate(oq.w8a16(a, attn.wq.weight, attn.wq.scales).view(M, Hq, 1, D), oc, os_)
+    rk = orope.rotate(oq.w8a16(a, attn.wk.weight, attn.wk.scales).view(M, Hkv, 1, D), oc, os_)
+    rv = oq.w8a16(a, attn.wv.weight, attn.wv.scales).view(M, Hkv, D)
+    assert q.shape == (M, Hq, 1, D)
+    _close(q, rq, 2e-2)
+    _close(cache.k[layer, :M, :, p], rk[:, :, 0], 2e-2)
+    _close(cache.v[layer, :M, :, p], rv, 2e-2)
+    # every other slot (other positions, rows >= M, other layers) is untouched
+    mask = torch.ones_like(cache.k, dtype=torch.bool)
+    mask[layer, :M, :, p] = False
+    assert torch.equal(cache.k[mask], k0[mask]) and torch.equal(cache.v[mask], v0[mask])
+    # unfused GPU chain: GEMV kernel then the RoPE kernel on the same rounded values
+    from src.rms_norm import rmsnorm_triton
+    xn = rmsnorm_triton(x, nw, 1e-5)
+    uq = apply_rotary(attn.wq(xn).view(M, 1, Hq, D).transpose(1, 2), *table.rows(p, 1))
+    _close(q, uq, 1e-2)
+
+
+def test_qkv_position_outside_cache_writes_nothing(dev):
+    from src import decode_layer
+    from src.rope import DeviceRopeTable
+    dtype, M, Hq, Hkv, D, dim, T = torch.bfloat16, 4, 8, 2, 64, 256, 64
+    attn = _Attn(dev, dim, Hq, Hkv, D, dtype)
+    cache = _Cache(dev, 1, M, Hkv, T, D, dtype)
+    k0, v0 = cache.k.clone(), cache.v.clone()
+    table = DeviceRopeTable(orope.freqs_cis(D, T, 500000.0), dtype, dev)
+    x = randn((M, dim), 41, dtype, dev)
+    for p in (T, T + 5):
+        pos = torch.full((1,), p, dtype=torch.int64, device=dev)
+        q = decode_layer.qkv_rope_append(x, attn, None, 0.0, table.cos, table.sin, 0, pos, cache, 0)
+        torch.cuda.synchronize()
+        assert torch.isfinite(q.float()).all()
+    assert torch.equal(cache.k, k0) and torch.equal(cache.v, v0)
+
+
+def test_fused_decode_step_matches_unfused(dev):
+    """The quantized block's fused single-token path against the op-by-op
+    composition of the same model (eager, three decode steps)."""
+    from src.config import ModelArgs
+    from src.kv_cache import KVCache
+    from src.model_quantized import QuantizedTransformerBlock, build_random_quantized
+    args = ModelArgs(dim=512, n_layers=2, n_heads=8, n_kv_heads=2, vocab_size=1000, hidden_dim=1024,
+                     max_batch_size=4, max_seq_len=128, device=str(dev))
+    model = build_random_quantized(args, seed=3, device=str(dev))
+    kv_a, kv_b = KVCache(args, dtype=torch.bfloat16), KVCache(args, dtype=torch.bfloat16)
+    toks = torch.randint(0, args.vocab_size, (4, 20), generator=torch.Generator().manual_seed(5)).to(dev)
+    with torch.no_grad():
+        model(toks, start_pos=0, kv_cache=kv_a)
+        kv_b.k.copy_(kv_a.k)
+        kv_b.v.copy_(kv_a.v)
+        for step in range(3):
+            tok = toks[:, step:step + 1]
+            QuantizedTransformerBlock.fused_decode = True
+            la = model(tok, start_pos=20 + step, kv_cache=kv_a)
+            QuantizedTransformerBlock.fused_decode = False
+            try:
+                lb = model(tok, start_pos=20 + step, kv_cache=kv_b)
+            finally:
+                QuantizedTransformerBlock.fused_decode = True
+            _close(la, lb, 1e-2)
+            _close(kv_a.k, kv_b.k, 1e-2)
+            _close(kv_a.v, kv_b.v, 1e-2)
