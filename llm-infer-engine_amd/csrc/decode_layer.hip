@@ -101,32 +101,49 @@ __device__ inline float silu_f32(float a) { return a / (1.0f + expf(-a)); }
 // Weight row of tile row r (0..15) for tile `tile`: rows 0..RPB-1 of the tile;
 // for the RoPE epilogue a tile holds 8 rotation pairs: rows i and i+8 are head
 // dims d and d + D/2.
-template <int EPI>
+template <int EPI, int RPB>
 __device__ inline int tile_row(int tile_in_mat, int r, int D) {
   if constexpr (EPI == kEpiQkvRope) {
     const int half = D >> 1, tiles_per_head = half >> 3;
     const int head = tile_in_mat / tiles_per_head, j = tile_in_mat % tiles_per_head;
     return head * D + 8 * j + (r & 7) + ((r >> 3) ? half : 0);
   } else {
-    return tile_in_mat * 16 + r;
+    return tile_in_mat * RPB + r;
   }
 }
 
-template <typename T, int NW, int MAXC, bool NORM, int EPI>
+template <typename T, int NW, bool NORM, int EPI, int RPB, int MR>
 __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
   using MM = LMfma<T>;
   typedef typename MM::v8 v8;
   constexpr int NMAT = EPI == kEpiSwiglu ? 2 : 1;      // A streams per tile
-  // MAXC: 64-k chunks per wave (NW * MAXC covers K)
+  constexpr int MAXC = 8;          // 64-k chunks per wave: K = 512 * NW (host-checked)
+  // MR: rows of x the RMSNorm prologue holds (>= M)
   extern __shared__ __align__(16) unsigned char smem[];
   T* xs = reinterpret_cast<T*>(smem);                   // NORM: [M][K] normalised x
-  f32x4* red = reinterpret_cast<f32x4*>(smem + (NORM ? (size_t)a.M * a.K * sizeof(T) : 0));
+  float* red_ss = reinterpret_cast<float*>(smem + (NORM ? (size_t)a.M * a.K * sizeof(T) : 0));
+  f32x4* red = reinterpret_cast<f32x4*>(smem + (NORM ? (size_t)a.M * a.K * sizeof(T) +
+                                                           (size_t)NW * MR * sizeof(float)
+                                                     : 0));
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;    // A: weight row in tile / k group
   const int m = lane & 15;                   // B: x row
   const bool m_ok = m < a.M;
+
+  // ---- RMSNorm prologue, part 1: this thread's 16-byte column chunk of every
+  //      x row (and of the norm weight), requested before any weight load so
+  //      the statistics do not wait behind the weight stream (vmcnt retires
+  //      in order).  K = 8 * 64 * NW: one chunk per thread per row.
+  u32x4 xv[NORM ? MR : 1], nwv = {0, 0, 0, 0};
+  if constexpr (NORM) {
+#pragma unroll
+    for (int row = 0; row < MR; ++row)
+      xv[row] = row < a.M ? load16(reinterpret_cast<const T*>(a.x) + (int64_t)row * a.x_sm + tid * 8)
+                          : u32x4{0, 0, 0, 0};
+    nwv = load16(reinterpret_cast<const T*>(a.norm_w) + tid * 8);
+  }
 
   // ---- which matrix / tile this block owns
   int tile = blockIdx.x;
@@ -140,50 +157,58 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
   }
   const int8_t* wm = mat == 0 ? a.w0 : (mat == 1 ? a.w1 : a.w2);
   const int64_t w_sn = mat == 0 ? a.w_sn0 : (mat == 1 ? a.w_sn1 : a.w_sn2);
-  const int n_in_mat = tile_row<EPI>(tile, r, a.D);     // this lane's weight row
+  const int n_in_mat = tile_row<EPI, RPB>(tile, r, a.D);   // this lane's weight row
   const int n_valid = EPI == kEpiQkvRope ? (mat == 0 ? a.Hq : a.Hkv) * a.D : a.N;
-  const bool row_ok = n_in_mat < n_valid;
+  const bool row_ok = r < RPB && n_in_mat < n_valid;
   const int8_t* wrow0 = wm + (int64_t)(row_ok ? n_in_mat : 0) * w_sn;
   const int8_t* wrow1 = NMAT == 2 ? a.w1 + (int64_t)(row_ok ? n_in_mat : 0) * a.w_sn1 : nullptr;
 
-  // ---- issue every weight load of this wave's K slice
-  const int n_chunks = a.K >> 6;                        // K % 64 == 0 (host-checked)
-  const int cpw = (n_chunks + NW - 1) / NW;
-  const int c_lo = w * cpw, c_hi = min(c_lo + cpw, n_chunks);
+  // ---- issue every weight load of this wave's K slice (MAXC chunks of 64)
+  const int c_lo = w * MAXC;
   u32x4 wq[NMAT][MAXC];
 #pragma unroll
   for (int i = 0; i < MAXC; ++i) {
-    const int c = c_lo + i;
-    const bool ok = c < c_hi && row_ok;
-    const int k0 = c * 64 + 16 * g;
-    wq[0][i] = ok ? load16_stream(wrow0 + k0) : u32x4{0, 0, 0, 0};
-    if constexpr (NMAT == 2) wq[1][i] = ok ? load16_stream(wrow1 + k0) : u32x4{0, 0, 0, 0};
+    const int k0 = (c_lo + i) * 64 + 16 * g;
+    wq[0][i] = row_ok ? load16_stream(wrow0 + k0) : u32x4{0, 0, 0, 0};
+    if constexpr (NMAT == 2) wq[1][i] = row_ok ? load16_stream(wrow1 + k0) : u32x4{0, 0, 0, 0};
   }
 
-  // ---- RMSNorm prologue: normalised rows into LDS (overlaps the loads above)
+  // ---- RMSNorm prologue, part 2: per-row sum of squares (wave shuffles, then
+  //      LDS across waves), normalised rows into LDS, rounded to T
   if constexpr (NORM) {
-    const T* nw = reinterpret_cast<const T*>(a.norm_w);
-    for (int row = w; row < a.M; row += NW) {
-      const T* xr = reinterpret_cast<const T*>(a.x) + (int64_t)row * a.x_sm;
-      float ss = 0.f;
-      for (int k = lane * 8; k < a.K; k += 512) {
+    float ss[MR];
+#pragma unroll
+    for (int row = 0; row < MR; ++row) {
+      float v[8];
+      Chunk<T>::unpack(xv[row], v);
+      float t = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) t = fmaf(v[e], v[e], t);
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) t += shfl_xor_f32(t, off);
+      ss[row] = t;
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int row = 0; row < MR; ++row) red_ss[w * MR + row] = ss[row];
+    }
+    __syncthreads();
+    float wn[8];
+    Chunk<T>::unpack(nwv, wn);
+#pragma unroll
+    for (int row = 0; row < MR; ++row) {
+      if (row < a.M) {
+        float tot = 0.f;
+  #pragma unroll
+        for (int ww = 0; ww < NW; ++ww) tot += red_ss[ww * MR + row];
+        const float rstd = 1.0f / sqrtf(tot / (float)a.K + a.eps);
         float v[8];
-        Chunk<T>::unpack(load16(xr + k), v);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
-      }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) ss += shfl_xor_f32(ss, off);
-      const float rstd = 1.0f / sqrtf(ss / (float)a.K + a.eps);
-      for (int k = lane * 8; k < a.K; k += 512) {
-        float v[8], wv[8];
-        Chunk<T>::unpack(load16(xr + k), v);
-        Chunk<T>::unpack(load16(nw + k), wv);
+        Chunk<T>::unpack(xv[row], v);
         typedef T t8 __attribute__((ext_vector_type(8)));
         t8 o;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = Elem<T>::from_f32(v[e] * rstd * wv[e]);
-        *reinterpret_cast<t8*>(xs + (int64_t)row * a.K + k) = o;
+  #pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = Elem<T>::from_f32(v[e] * rstd * wn[e]);
+        *reinterpret_cast<t8*>(xs + (int64_t)row * a.K + tid * 8) = o;
       }
     }
     __syncthreads();
@@ -196,9 +221,7 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
   for (int t = 0; t < NMAT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < MAXC; ++i) {
-    const int c = c_lo + i;
-    if (c >= c_hi) break;
-    const int k0 = c * 64 + 16 * g;
+    const int k0 = (c_lo + i) * 64 + 16 * g;
     v8 xb0, xb1;
     if (m_ok) {
       const T* xp = NORM ? xs + (int64_t)m * a.K + k0 : xg + k0;
@@ -286,8 +309,9 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
     if (!m_ok) return;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int n = tile * 16 + 4 * g + i;
-      if (n >= a.N) continue;
+      const int rr = 4 * g + i;
+      const int n = tile * RPB + rr;
+      if (rr >= RPB || n >= a.N) continue;
       float v = Elem<T>::to_f32(Elem<T>::from_f32(acc[0][i] * scale_of(a.s0, n)));
       if constexpr (EPI == kEpiResidual) {
         const float rv = Elem<T>::to_f32(reinterpret_cast<const T*>(a.res)[(int64_t)m * a.res_sm + n]);
@@ -304,31 +328,58 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
 
 namespace {
 
-template <typename T, int NW, int MAXC, bool NORM, int EPI>
+template <typename T, int NW, bool NORM, int EPI, int RPB, int MR>
 hipError_t launch_layer_gemv(const LayerGemvArgs& a, int n_blocks, hipStream_t st) {
   size_t smem = (size_t)(NW - 1) * (EPI == kEpiSwiglu ? 2 : 1) * 64 * sizeof(f32x4);
-  if (NORM) smem += (size_t)a.M * a.K * sizeof(T);
-  hipLaunchKernelGGL((layer_gemv_kernel<T, NW, MAXC, NORM, EPI>), dim3((unsigned)n_blocks),
+  if (NORM) smem += (size_t)a.M * a.K * sizeof(T) + (size_t)NW * MR * sizeof(float);
+  hipLaunchKernelGGL((layer_gemv_kernel<T, NW, NORM, EPI, RPB, MR>), dim3((unsigned)n_blocks),
                      dim3(64 * NW), smem, st, a);
   return hipGetLastError();
 }
 
-// Waves per block and 64-k chunks per wave: each wave's slice of K is loaded
-// in one go (MAXC registers of 16 bytes per lane and matrix).
-template <typename T, bool NORM, int EPI>
+// Waves per block: K = 512 * NW (each wave owns 8 chunks of 64 k).  The
+// RMSNorm prologue keeps MR (8 or 16 >= M) rows of one column chunk per thread.
+template <typename T, bool NORM, int EPI, int RPB>
 hipError_t dispatch_nw(const LayerGemvArgs& a, int n_blocks, hipStream_t st) {
-  const int chunks = a.K / 64;
-  if (chunks <= 4 * 8) return launch_layer_gemv<T, 4, 8, NORM, EPI>(a, n_blocks, st);
-  if (chunks <= 8 * 8) return launch_layer_gemv<T, 8, 8, NORM, EPI>(a, n_blocks, st);
-  if (EPI == kEpiSwiglu || chunks <= 8 * 16)  // SwiGLU: K <= 8192 (host-checked)
-    return launch_layer_gemv<T, 8, 16, NORM, EPI>(a, n_blocks, st);
-  return launch_layer_gemv<T, 16, 16, NORM, EPI>(a, n_blocks, st);
+  constexpr int MR = 8;
+  if (NORM && a.M > MR) {
+    switch (a.K) {
+      case 512: return launch_layer_gemv<T, 1, NORM, EPI, RPB, 16>(a, n_blocks, st);
+      case 1024: return launch_layer_gemv<T, 2, NORM, EPI, RPB, 16>(a, n_blocks, st);
+      case 2048: return launch_layer_gemv<T, 4, NORM, EPI, RPB, 16>(a, n_blocks, st);
+      default: return hipErrorInvalidValue;  // host checks exclude the rest
+    }
+  }
+  switch (a.K) {
+    case 512: return launch_layer_gemv<T, 1, NORM, EPI, RPB, MR>(a, n_blocks, st);
+    case 1024: return launch_layer_gemv<T, 2, NORM, EPI, RPB, MR>(a, n_blocks, st);
+    case 1536: return launch_layer_gemv<T, 3, NORM, EPI, RPB, MR>(a, n_blocks, st);
+    case 2048: return launch_layer_gemv<T, 4, NORM, EPI, RPB, MR>(a, n_blocks, st);
+    case 3072: return launch_layer_gemv<T, 6, NORM, EPI, RPB, MR>(a, n_blocks, st);
+    case 4096: return launch_layer_gemv<T, 8, NORM, EPI, RPB, MR>(a, n_blocks, st);
+    case 6144: return launch_layer_gemv<T, 12, NORM, EPI, RPB, MR>(a, n_blocks, st);
+    case 8192: return launch_layer_gemv<T, 16, NORM, EPI, RPB, MR>(a, n_blocks, st);
+    default: return hipErrorInvalidValue;
+  }
 }
 
-template <typename T, int EPI>
+template <typename T, int EPI, int RPB>
 hipError_t dispatch_norm(const LayerGemvArgs& a, int n_blocks, hipStream_t st) {
-  return a.norm_w != nullptr ? dispatch_nw<T, true, EPI>(a, n_blocks, st)
-                             : dispatch_nw<T, false, EPI>(a, n_blocks, st);
+  return a.norm_w != nullptr ? dispatch_nw<T, true, EPI, RPB>(a, n_blocks, st)
+                             : dispatch_nw<T, false, EPI, RPB>(a, n_blocks, st);
+}
+
+// Row tiles of 16 when that already makes a few hundred blocks, else of 8
+// (the A rows beyond 8 are zero) so that small-N projections use every CU.
+template <typename T, int EPI>
+hipError_t dispatch_tile(const LayerGemvArgs& a, hipStream_t st) {
+  if (a.N / 16 >= 240) return dispatch_norm<T, EPI, 16>(a, (a.N + 15) / 16, st);
+  return dispatch_norm<T, EPI, 8>(a, (a.N + 7) / 8, st);
+}
+
+bool k_supported(int64_t K) {
+  return K == 512 || K == 1024 || K == 1536 || K == 2048 || K == 3072 || K == 4096 ||
+         K == 6144 || K == 8192;
 }
 
 int32_t check_x(const void* x, int64_t M, int64_t K, int64_t x_sm, const void* norm_w,
@@ -341,18 +392,19 @@ int32_t check_x(const void* x, int64_t M, int64_t K, int64_t x_sm, const void* n
     set_last_error("%s: activations must be bf16 or fp16 (dtype %d)", what, (int)dtype);
     return MI_ERR_UNSUPPORTED;
   }
-  if (M < 1 || M > 16 || K < 64 || K % 64 != 0 || K > 16 * 16 * 64) {
-    set_last_error("%s: need 1 <= M <= 16 and K a multiple of 64 up to 16384 (M=%lld K=%lld)",
-                   what, (long long)M, (long long)K);
+  if (M < 1 || M > 16 || !k_supported(K)) {
+    set_last_error("%s: need 1 <= M <= 16 and K in {512, 1024, 1536, 2048, 3072, 4096, 6144, "
+                   "8192} (M=%lld K=%lld)", what, (long long)M, (long long)K);
     return MI_ERR_UNSUPPORTED;
   }
   if ((uintptr_t)x % 16 != 0 || (x_sm * 2) % 16 != 0) {
     set_last_error("%s: x rows must be 16-byte aligned", what);
     return MI_ERR_INVALID;
   }
-  if (norm_w != nullptr && ((uintptr_t)norm_w % 16 != 0 || M * K * 2 > 64 * 1024)) {
-    set_last_error("%s: RMSNorm prologue needs a 16-byte aligned weight and M*K*2 <= 64 KB",
-                   what);
+  if (norm_w != nullptr && ((uintptr_t)norm_w % 16 != 0 || M * K * 2 > 64 * 1024 ||
+                            (M > 8 && K > 2048))) {
+    set_last_error("%s: RMSNorm prologue needs a 16-byte aligned weight, M*K*2 <= 64 KB and "
+                   "K <= 2048 for M > 8", what);
     return MI_ERR_UNSUPPORTED;
   }
   return MI_OK;
@@ -393,8 +445,9 @@ extern "C" int32_t mi_w8a16_linear_fused(
     return MI_ERR_INVALID;
   }
   if (epilogue == kEpiSwiglu && (st = check_w(w_b, s_b, w_sn_b, what)) != MI_OK) return st;
-  if (epilogue == kEpiSwiglu && K > 8192) {
-    set_last_error("%s: SwiGLU epilogue supports K <= 8192 (K=%lld)", what, (long long)K);
+  if (epilogue == kEpiSwiglu && norm_w != nullptr && K > 4096) {
+    set_last_error("%s: SwiGLU with the RMSNorm prologue supports K <= 4096 (K=%lld)", what,
+                   (long long)K);
     return MI_ERR_UNSUPPORTED;
   }
   if (epilogue != kEpiStore && epilogue != kEpiResidual && epilogue != kEpiSwiglu) {
@@ -407,17 +460,16 @@ extern "C" int32_t mi_w8a16_linear_fused(
   a.w1 = w_b; a.s1 = s_b; a.w_sn1 = w_sn_b;
   a.y = y; a.res = res; a.x_sm = x_sm; a.y_sm = y_sm; a.res_sm = res_sm;
   a.M = (int32_t)M; a.K = (int32_t)K; a.N = (int32_t)N;
-  const int n_blocks = (int)((N + 15) / 16);
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (dtype == MI_DTYPE_BF16) {
-    e = epilogue == kEpiStore ? dispatch_norm<bf16_t, kEpiStore>(a, n_blocks, s)
-        : epilogue == kEpiResidual ? dispatch_norm<bf16_t, kEpiResidual>(a, n_blocks, s)
-                                   : dispatch_norm<bf16_t, kEpiSwiglu>(a, n_blocks, s);
+    e = epilogue == kEpiStore ? dispatch_tile<bf16_t, kEpiStore>(a, s)
+        : epilogue == kEpiResidual ? dispatch_tile<bf16_t, kEpiResidual>(a, s)
+                                   : dispatch_tile<bf16_t, kEpiSwiglu>(a, s);
   } else {
-    e = epilogue == kEpiStore ? dispatch_norm<f16_t, kEpiStore>(a, n_blocks, s)
-        : epilogue == kEpiResidual ? dispatch_norm<f16_t, kEpiResidual>(a, n_blocks, s)
-                                   : dispatch_norm<f16_t, kEpiSwiglu>(a, n_blocks, s);
+    e = epilogue == kEpiStore ? dispatch_tile<f16_t, kEpiStore>(a, s)
+        : epilogue == kEpiResidual ? dispatch_tile<f16_t, kEpiResidual>(a, s)
+                                   : dispatch_tile<f16_t, kEpiSwiglu>(a, s);
   }
   if (e != hipSuccess) {
     set_last_error("%s: launch failed: %s", what, hipGetErrorString(e));
@@ -468,8 +520,8 @@ extern "C" int32_t mi_w8a16_qkv_rope_append(
   a.n_tiles1 = (int32_t)(n_kv_heads * tph);
   const int n_blocks = a.n_tiles0 + 2 * a.n_tiles1;
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e = dtype == MI_DTYPE_BF16 ? dispatch_norm<bf16_t, kEpiQkvRope>(a, n_blocks, s)
-                                        : dispatch_norm<f16_t, kEpiQkvRope>(a, n_blocks, s);
+  hipError_t e = dtype == MI_DTYPE_BF16 ? dispatch_norm<bf16_t, kEpiQkvRope, 16>(a, n_blocks, s)
+                                        : dispatch_norm<f16_t, kEpiQkvRope, 16>(a, n_blocks, s);
   if (e != hipSuccess) {
     set_last_error("%s: launch failed: %s", what, hipGetErrorString(e));
     return (int32_t)e;

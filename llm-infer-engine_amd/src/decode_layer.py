@@ -29,14 +29,19 @@ def _w(lin):
     return lin.weight, lin.scales.reshape(-1)
 
 
-def supported(M: int, K: int, dtype: torch.dtype, lin, norm_weight=None) -> bool:
+#: reduction lengths the fused GEMV kernels are built for (K = 512 * waves)
+SUPPORTED_K = (512, 1024, 1536, 2048, 3072, 4096, 6144, 8192)
+
+
+def supported(M: int, K: int, dtype: torch.dtype, lin, norm_weight=None, *,
+              swiglu: bool = False) -> bool:
     """Whether the fused kernels take an [M, K] input of `dtype` through W8A16
     layer `lin` (and RMSNorm weight `norm_weight`); the input itself must also
     be row-aligned (``aligned``).  Otherwise use the op-by-op path."""
     if dtype not in (torch.bfloat16, torch.float16):
         return False
     w, s = _w(lin)
-    if not (1 <= M <= 16 and K % 64 == 0 and K <= 16384 and w.dtype == torch.int8):
+    if not (1 <= M <= 16 and K in SUPPORTED_K and w.dtype == torch.int8):
         return False
     if not (w.is_contiguous() and w.shape[1] == K and w.data_ptr() % 16 == 0):
         return False
@@ -44,7 +49,8 @@ def supported(M: int, K: int, dtype: torch.dtype, lin, norm_weight=None) -> bool
         return False
     if norm_weight is not None:
         if (norm_weight.dtype != dtype or not norm_weight.is_contiguous()
-                or norm_weight.data_ptr() % 16 != 0 or M * K * 2 > 64 * 1024):
+                or norm_weight.data_ptr() % 16 != 0 or M * K * 2 > 64 * 1024
+                or (M > 8 and K > 2048) or (swiglu and K > 4096)):
             return False
     return True
 

@@ -56,7 +56,8 @@ class QuantizedTransformerBlock(TransformerBlock):
                 and sup(B, dim, dt, attn.wq, self.attention_norm.weight)
                 and sup(B, dim, dt, attn.wk) and sup(B, dim, dt, attn.wv)
                 and sup(B, n_o, dt, attn.wo)
-                and sup(B, dim, dt, ff.w1, self.ffn_norm.weight) and sup(B, dim, dt, ff.w3)
+                and sup(B, dim, dt, ff.w1, self.ffn_norm.weight, swiglu=True)
+                and sup(B, dim, dt, ff.w3)
                 and sup(B, ff.w1.out_features, dt, ff.w2))
 
     def forward(self, x, rope_cos, rope_sin, layer_idx=None, start_pos=0, kv_cache=None,

@@ -32,12 +32,12 @@ def _close(a, b, tol):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("M,K,N", [(1, 256, 384), (3, 2048, 512), (8, 2048, 2048), (16, 1024, 256),
-                                   (8, 8192, 2048)])
+@pytest.mark.parametrize("M,K,N", [(1, 512, 384), (3, 2048, 512), (8, 2048, 2048), (16, 1024, 256),
+                                   (8, 8192, 2048), (12, 2048, 4096), (5, 3072, 600)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_linear_store_and_residual(dev, dtype, M, K, N, norm):
-    if norm and M * K * 2 > 64 * 1024:
-        pytest.skip("the RMSNorm prologue stages at most 64 KB of rows")
+    if norm and (M * K * 2 > 64 * 1024 or (M > 8 and K > 2048)):
+        pytest.skip("the RMSNorm prologue stages at most 64 KB of rows (K <= 2048 above 8 rows)")
     from src import decode_layer
     from src.rms_norm import rmsnorm_triton
     lin = _linear(dev, K, N, dtype, 1)
@@ -127,10 +127,23 @@ def test_qkv_rope_append(dev, dtype, M, Hq, Hkv, D, by_position):
     _close(q, uq, 1e-2)
 
 
+def test_unsupported_shapes_are_rejected(dev):
+    """K outside the built set, M > 16: the C side refuses (nothing launched)
+    and the model-level predicate routes such calls to the op chain."""
+    from src import decode_layer
+    lin = _linear(dev, 256, 64, torch.bfloat16, 9)
+    x = randn((4, 256), 10, torch.bfloat16, dev)
+    assert not decode_layer.supported(4, 256, torch.bfloat16, lin)
+    with pytest.raises(NotImplementedError):
+        decode_layer.linear_fused(x, lin)
+    lin2 = _linear(dev, 512, 64, torch.bfloat16, 9)
+    assert not decode_layer.supported(17, 512, torch.bfloat16, lin2)
+
+
 def test_qkv_position_outside_cache_writes_nothing(dev):
     from src import decode_layer
     from src.rope import DeviceRopeTable
-    dtype, M, Hq, Hkv, D, dim, T = torch.bfloat16, 4, 8, 2, 64, 256, 64
+    dtype, M, Hq, Hkv, D, dim, T = torch.bfloat16, 4, 8, 2, 64, 512, 64
     attn = _Attn(dev, dim, Hq, Hkv, D, dtype)
     cache = _Cache(dev, 1, M, Hkv, T, D, dtype)
     k0, v0 = cache.k.clone(), cache.v.clone()
