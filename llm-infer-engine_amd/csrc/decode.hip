@@ -10,15 +10,19 @@
 //     128-bit global loads; a row of D elements spans LPR = D*sizeof(T)/16
 //     lanes, capped at 16 = one DPP row);
 //   * q.k row sums use DPP row reductions (no LDS round trip), the softmax is
-//     kept per 16-lane row group in registers (log2 domain, v_exp_f32), and the
-//     groups/waves are merged once at the end through LDS;
+//     kept per row group in registers (log2 domain, v_exp_f32); the row
+//     groups of a wave merge through DPP / permlane swaps and the waves once
+//     through LDS;
 //   * no MFMA: at one query token per head there is nothing to amortise a
 //     matrix tile over, and the loop is HBM-bound.
-// Keys beyond seq_lens[b] are never loaded (the grid is static so the launch
-// is hipGraph-safe; surplus splits just publish an empty partial).
+// Keys beyond seq_lens[b] are never loaded.  The grid is static (sized for
+// the capacity, so the launch is hipGraph-safe) and with seq_lens the splits
+// divide each sequence's own length, so a replay at any length keeps every
+// split busy.
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -91,6 +95,26 @@ __device__ inline float dot_chunk<float>(const u32x4& q, const u32x4& k,
   return acc;
 }
 
+// x from lane (lane ^ OFF): a DPP row rotate for 8, the permlane swaps for 16
+// and 32 (no LDS traffic); a ds_bpermute for the small strides.
+template <int OFF>
+__device__ inline float lane_xor(float x, int lane) {
+  if constexpr (OFF == 8) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, true));
+  } else if constexpr (OFF == 16) {
+    auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x),
+                                               __float_as_uint(x), false, false);
+    return __uint_as_float((lane & 16) ? sw[0] : sw[1]);
+  } else if constexpr (OFF == 32) {
+    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x),
+                                               __float_as_uint(x), false, false);
+    return __uint_as_float((lane & 32) ? sw[0] : sw[1]);
+  } else {
+    return shfl_xor_f32(x, OFF);
+  }
+}
+
 template <typename T, int D>
 struct DecodeGeom {
   static constexpr int kEPC = 16 / Elem<T>::kBytes;       // elems per chunk
@@ -129,23 +153,36 @@ __global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
     const int64_t sl = a.seq_lens[b];
     leff = (int)(sl < 0 ? 0 : (sl < leff ? sl : leff));
   }
-  const int start = split * a.split_len;
-  const int end = min(start + a.split_len, leff);
+  // With per-sequence lengths the splits divide each sequence's own keys
+  // (the grid is sized for the capacity, so a graph replay at any length
+  // keeps every split busy); otherwise they tile kv_len.
+  int split_len = a.split_len;
+  if (a.seq_lens != nullptr)
+    split_len = ((leff + a.num_splits - 1) / a.num_splits + 15) & ~15;
+  const int start = split * split_len;
+  const int end = min(start + split_len, leff);
 
   // q chunks for this lane, raw (q.k is done on the stored precision, fp32
   // accumulate, exactly like sum(k.f32 * q.f32) in the reference).
+  // All heads' loads are issued before the first wait (one round trip).
   u32x4 qr[GC][CPL];
+  if (a.q_vec) {
 #pragma unroll
-  for (int g = 0; g < GC; ++g) {
-    const int h = h0 + min(g, ng - 1);
-    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
-                  (int64_t)h * a.q_sh;
+    for (int g = 0; g < GC; ++g) {
+      const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                    (int64_t)(h0 + min(g, ng - 1)) * a.q_sh;
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int d0 = (li + j * LPR) * EPC;
-      if (a.q_vec) {
-        qr[g][j] = *reinterpret_cast<const u32x4*>(qp + d0);
-      } else {
+      for (int j = 0; j < CPL; ++j)
+        qr[g][j] = *reinterpret_cast<const u32x4*>(qp + (li + j * LPR) * EPC);
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < GC; ++g) {
+      const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                    (int64_t)(h0 + min(g, ng - 1)) * a.q_sh;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int d0 = (li + j * LPR) * EPC;
         union { u32x4 u; T t[EPC]; } tmp;
 #pragma unroll
         for (int e = 0; e < EPC; ++e) tmp.t[e] = qp[(int64_t)(d0 + e) * a.q_sd];
@@ -241,23 +278,27 @@ __global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
   }
 
   // Merge the RPW row groups of this wave (butterfly over lane strides).
-#pragma unroll
-  for (int off = LPR; off < 64; off <<= 1) {
+  auto merge_off = [&](auto off_c) {
+    constexpr int OFF = decltype(off_c)::value;
 #pragma unroll
     for (int g = 0; g < GC; ++g) {
-      const float mo = shfl_xor_f32(m[g], off);
-      const float lo = shfl_xor_f32(l[g], off);
+      const float mo = lane_xor<OFF>(m[g], lane);
+      const float lo = lane_xor<OFF>(l[g], lane);
       const float mn = fmaxf(m[g], mo);
       const float wa = fast_exp2(m[g] - mn), wb = fast_exp2(mo - mn);
       l[g] = l[g] * wa + lo * wb;
 #pragma unroll
-      for (int e = 0; e < E; ++e) {
-        const float ao = shfl_xor_f32(acc[g][e], off);
-        acc[g][e] = acc[g][e] * wa + ao * wb;
-      }
+      for (int e = 0; e < E; ++e)
+        acc[g][e] = acc[g][e] * wa + lane_xor<OFF>(acc[g][e], lane) * wb;
       m[g] = mn;
     }
-  }
+  };
+  if constexpr (LPR <= 1) merge_off(std::integral_constant<int, 1>{});
+  if constexpr (LPR <= 2) merge_off(std::integral_constant<int, 2>{});
+  if constexpr (LPR <= 4) merge_off(std::integral_constant<int, 4>{});
+  if constexpr (LPR <= 8) merge_off(std::integral_constant<int, 8>{});
+  if constexpr (LPR <= 16) merge_off(std::integral_constant<int, 16>{});
+  merge_off(std::integral_constant<int, 32>{});
 
   // Cross-wave merge through LDS: [nw][GC] m, l and [nw][GC][D] acc.
   float* sm_m = smem;

@@ -136,12 +136,16 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
   //      x row (and of the norm weight), requested before any weight load so
   //      the statistics do not wait behind the weight stream (vmcnt retires
   //      in order).  K = 8 * 64 * NW: one chunk per thread per row.
+  //      Every load in this kernel is unconditional (rows beyond M or N read
+  //      a clamped row and are discarded by the epilogue): a load under a
+  //      branch forces the compiler's vmcnt waits to assume it was skipped,
+  //      which would make the first wait cover the whole weight stream.
   u32x4 xv[NORM ? MR : 1], nwv = {0, 0, 0, 0};
   if constexpr (NORM) {
 #pragma unroll
     for (int row = 0; row < MR; ++row)
-      xv[row] = row < a.M ? load16(reinterpret_cast<const T*>(a.x) + (int64_t)row * a.x_sm + tid * 8)
-                          : u32x4{0, 0, 0, 0};
+      xv[row] = load16(reinterpret_cast<const T*>(a.x) + (int64_t)min(row, a.M - 1) * a.x_sm +
+                       tid * 8);
     nwv = load16(reinterpret_cast<const T*>(a.norm_w) + tid * 8);
   }
 
@@ -163,15 +167,31 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
   const int8_t* wrow0 = wm + (int64_t)(row_ok ? n_in_mat : 0) * w_sn;
   const int8_t* wrow1 = NMAT == 2 ? a.w1 + (int64_t)(row_ok ? n_in_mat : 0) * a.w_sn1 : nullptr;
 
-  // ---- issue every weight load of this wave's K slice (MAXC chunks of 64)
+  // ---- without the prologue the B operands come straight from global memory:
+  //      request them all first (L2 hits, they retire ahead of the weights)
   const int c_lo = w * MAXC;
+  const int mc = min(m, a.M - 1);             // columns m >= M are discarded
+  const T* xg = reinterpret_cast<const T*>(a.x) + (int64_t)mc * a.x_sm;
+  u32x4 xr[NORM ? 1 : MAXC][2];
+  if constexpr (!NORM) {
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+      const int k0 = (c_lo + i) * 64 + 16 * g;
+      xr[i][0] = load16(xg + k0);
+      xr[i][1] = load16(xg + k0 + 8);
+    }
+  }
+
+  // ---- issue every weight load of this wave's K slice (MAXC chunks of 64)
   u32x4 wq[NMAT][MAXC];
 #pragma unroll
   for (int i = 0; i < MAXC; ++i) {
     const int k0 = (c_lo + i) * 64 + 16 * g;
-    wq[0][i] = row_ok ? load16_stream(wrow0 + k0) : u32x4{0, 0, 0, 0};
-    if constexpr (NMAT == 2) wq[1][i] = row_ok ? load16_stream(wrow1 + k0) : u32x4{0, 0, 0, 0};
+    wq[0][i] = load16_stream(wrow0 + k0);
+    if constexpr (NMAT == 2) wq[1][i] = load16_stream(wrow1 + k0);
   }
+  // keep the whole weight stream issued before the prologue's first wait
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- RMSNorm prologue, part 2: per-row sum of squares (wave shuffles, then
   //      LDS across waves), normalised rows into LDS, rounded to T
@@ -215,7 +235,6 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
   }
 
   // ---- MFMAs over the slice
-  const T* xg = reinterpret_cast<const T*>(a.x) + (int64_t)(m_ok ? m : 0) * a.x_sm;
   f32x4 acc[NMAT];
 #pragma unroll
   for (int t = 0; t < NMAT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -223,13 +242,13 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
   for (int i = 0; i < MAXC; ++i) {
     const int k0 = (c_lo + i) * 64 + 16 * g;
     v8 xb0, xb1;
-    if (m_ok) {
-      const T* xp = NORM ? xs + (int64_t)m * a.K + k0 : xg + k0;
+    if constexpr (NORM) {
+      const T* xp = xs + (int64_t)mc * a.K + k0;
       xb0 = __builtin_bit_cast(v8, load16(xp));
       xb1 = __builtin_bit_cast(v8, load16(xp + 8));
     } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) { xb0[e] = (T)0.f; xb1[e] = (T)0.f; }
+      xb0 = __builtin_bit_cast(v8, xr[i][0]);
+      xb1 = __builtin_bit_cast(v8, xr[i][1]);
     }
 #pragma unroll
     for (int t = 0; t < NMAT; ++t) {
