@@ -214,16 +214,18 @@ int32_t mi_w8a16_gemv(const void* x, const int8_t* w, const void* scales,
                       void* stream);
 
 /*
- * Fused decode-step projection (1 <= m <= 16 rows, k % 64 == 0, k <= 16384):
+ * Fused decode-step projection (1 <= m <= 16 rows; k one of 512, 1024, 1536,
+ * 2048, 3072, 4096, 6144, 8192):
  *   a   = rmsnorm(x, norm_w, eps) if norm_w != NULL else x   (rounded to dtype)
  *   y_a = dtype((sum_k a[m,k] * w_a[n,k]) * s_a[n])
  * then, by epilogue:
  *   0  y = y_a
  *   1  y = dtype(res + y_a)                                   (residual add)
- *   2  y = dtype(dtype(silu(y_a)) * y_b), y_b from w_b / s_b  (SwiGLU, k <= 8192)
+ *   2  y = dtype(dtype(silu(y_a)) * y_b), y_b from w_b / s_b  (SwiGLU, k <= 4096)
  * Weights int8 [n, k] with 16-byte aligned rows (row strides w_sn_* bytes),
  * scales in the activation dtype (bf16/fp16), x/res/y rows in elements.  With
- * norm_w, m*k*2 <= 64 KB.  Each step rounds where the reference's separate ops
+ * norm_w, m*k*2 <= 64 KB and k <= 2048 above 8 rows.  Unsupported shapes
+ * return MI_ERR_UNSUPPORTED.  Each step rounds where the reference's separate ops
  * round, so results equal the unfused chain up to fp32 summation order.
  * Replaces, fused into one launch: rmsnorm_triton  src/rms_norm.py:42-77;
  *   W8A16Linear / w8a16_gemv_launch  src/quant_linear.py:66-120, :250-292;

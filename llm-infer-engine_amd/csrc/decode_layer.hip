@@ -149,6 +149,10 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
     nwv = load16(reinterpret_cast<const T*>(a.norm_w) + tid * 8);
   }
 
+  // device position of the QKV epilogue (a scalar load, needed for the
+  // RoPE table addresses below)
+  const int64_t pos = EPI == kEpiQkvRope ? *a.pos : 0;
+
   // ---- which matrix / tile this block owns
   int tile = blockIdx.x;
   int mat = 0;
@@ -190,7 +194,41 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
     wq[0][i] = load16_stream(wrow0 + k0);
     if constexpr (NMAT == 2) wq[1][i] = load16_stream(wrow1 + k0);
   }
-  // keep the whole weight stream issued before the prologue's first wait
+  // ---- epilogue operands (row scales, residual, RoPE table entries), issued
+  //      behind the weights so the epilogue does not start with a round trip;
+  //      unconditional, from clamped indices (lanes beyond M / N discard them)
+  T e_s0[4], e_s1[4], e_res[4], e_cos[4], e_sin[4];
+  auto load_epilogue = [&]() {
+  if constexpr (EPI == kEpiQkvRope) {
+    const T* sc = reinterpret_cast<const T*>(mat == 0 ? a.s0 : (mat == 1 ? a.s1 : a.s2));
+    const int half = a.D >> 1, tph = half >> 3;
+    const int head = tile / tph, j8 = tile % tph;
+    // rows outside the table are clamped (callers keep positions in range)
+    const int64_t crow = min(max(pos - a.rope_row0, (int64_t)0), a.rope_rows - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = 4 * g + i;
+      e_s0[i] = sc[head * a.D + 8 * j8 + (rr & 7) + ((rr >> 3) ? half : 0)];
+      const int ii = 8 * j8 + 4 * (g & 1) + i;
+      e_cos[i] = reinterpret_cast<const T*>(a.cos)[crow * a.c_ss + ii];
+      e_sin[i] = reinterpret_cast<const T*>(a.sin)[crow * a.c_ss + ii];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int nc = min(tile * RPB + 4 * g + i, a.N - 1);
+      e_s0[i] = reinterpret_cast<const T*>(a.s0)[nc];
+      if constexpr (EPI == kEpiSwiglu) e_s1[i] = reinterpret_cast<const T*>(a.s1)[nc];
+      if constexpr (EPI == kEpiResidual)
+        e_res[i] = reinterpret_cast<const T*>(a.res)[(int64_t)mc * a.res_sm + nc];
+    }
+  }
+  };
+  // 1024-thread blocks (128 VGPRs) with a prologue or two weight streams have
+  // no registers to spare: they load these at the epilogue instead
+  constexpr bool kPrefetchEpi = !(NW >= 16 && (NORM || NMAT == 2));
+  if constexpr (kPrefetchEpi) load_epilogue();
+  // keep the whole load stream issued before the prologue's first wait
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- RMSNorm prologue, part 2: per-row sum of squares (wave shuffles, then
@@ -269,23 +307,18 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
 #pragma unroll
     for (int t = 0; t < NMAT; ++t) acc[t] += red[((ww - 1) * NMAT + t) * 64 + lane];
 
+  if constexpr (!kPrefetchEpi) load_epilogue();
   // acc[t][i] = C[tile row 4*g + i][x row m]
-  auto scale_of = [&](const void* s, int n) {
-    return Elem<T>::to_f32(reinterpret_cast<const T*>(s)[n]);
-  };
+  auto f32_of = [](T v) { return Elem<T>::to_f32(v); };
   if constexpr (EPI == kEpiQkvRope) {
     // rows 4g+i (g < 2) are dims d = 8j + 4g + i, their partners (rows +8) sit
     // in lane + 32: swap the rounded projections across the lane halves
-    const void* sc = mat == 0 ? a.s0 : (mat == 1 ? a.s1 : a.s2);
     const int half = a.D >> 1, tph = half >> 3;
     const int head = tile / tph, j8 = tile % tph;
     float yv[4], yp[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rr = 4 * g + i;
-      const int n = head * a.D + 8 * j8 + (rr & 7) + ((rr >> 3) ? half : 0);
-      yv[i] = Elem<T>::to_f32(Elem<T>::from_f32(acc[0][i] * scale_of(sc, n)));
-    }
+    for (int i = 0; i < 4; ++i)
+      yv[i] = Elem<T>::to_f32(Elem<T>::from_f32(acc[0][i] * f32_of(e_s0[i])));
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(yv[i]), __float_as_uint(yv[i]),
@@ -293,7 +326,7 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
       yp[i] = __uint_as_float(lane < 32 ? sw[1] : sw[0]);
     }
     if (!m_ok) return;
-    const int64_t p = *a.pos;
+    const int64_t p = pos;
     const bool hi = g >= 2;                       // rows 8..15: second half of the pair
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -303,10 +336,7 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
       if (mat == 2) {
         out = Elem<T>::from_f32(yv[i]);           // v: appended unrotated (bitwise)
       } else {
-        // rows outside the table are clamped (callers keep positions in range)
-        const int64_t crow = min(max(p - a.rope_row0, (int64_t)0), a.rope_rows - 1);
-        const float cs = Elem<T>::to_f32(reinterpret_cast<const T*>(a.cos)[crow * a.c_ss + ii]);
-        const float sn = Elem<T>::to_f32(reinterpret_cast<const T*>(a.sin)[crow * a.c_ss + ii]);
+        const float cs = f32_of(e_cos[i]), sn = f32_of(e_sin[i]);
         const float x1 = hi ? yp[i] : yv[i], x2 = hi ? yv[i] : yp[i];
         T y1, y2;
         {
@@ -331,12 +361,11 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
       const int rr = 4 * g + i;
       const int n = tile * RPB + rr;
       if (rr >= RPB || n >= a.N) continue;
-      float v = Elem<T>::to_f32(Elem<T>::from_f32(acc[0][i] * scale_of(a.s0, n)));
+      float v = Elem<T>::to_f32(Elem<T>::from_f32(acc[0][i] * f32_of(e_s0[i])));
       if constexpr (EPI == kEpiResidual) {
-        const float rv = Elem<T>::to_f32(reinterpret_cast<const T*>(a.res)[(int64_t)m * a.res_sm + n]);
-        v = Elem<T>::to_f32(Elem<T>::from_f32(rv + v));
+        v = Elem<T>::to_f32(Elem<T>::from_f32(f32_of(e_res[i]) + v));
       } else if constexpr (EPI == kEpiSwiglu) {
-        const float b = Elem<T>::to_f32(Elem<T>::from_f32(acc[1][i] * scale_of(a.s1, n)));
+        const float b = Elem<T>::to_f32(Elem<T>::from_f32(acc[1][i] * f32_of(e_s1[i])));
         const float sa = Elem<T>::to_f32(Elem<T>::from_f32(silu_f32(v)));
         v = sa * b;
       }
@@ -376,10 +405,16 @@ hipError_t dispatch_nw(const LayerGemvArgs& a, int n_blocks, hipStream_t st) {
     case 2048: return launch_layer_gemv<T, 4, NORM, EPI, RPB, MR>(a, n_blocks, st);
     case 3072: return launch_layer_gemv<T, 6, NORM, EPI, RPB, MR>(a, n_blocks, st);
     case 4096: return launch_layer_gemv<T, 8, NORM, EPI, RPB, MR>(a, n_blocks, st);
-    case 6144: return launch_layer_gemv<T, 12, NORM, EPI, RPB, MR>(a, n_blocks, st);
-    case 8192: return launch_layer_gemv<T, 16, NORM, EPI, RPB, MR>(a, n_blocks, st);
-    default: return hipErrorInvalidValue;
+    default: break;
   }
+  if constexpr (EPI != kEpiSwiglu) {  // two weight streams: K <= 4096 (host-checked)
+    switch (a.K) {
+      case 6144: return launch_layer_gemv<T, 12, NORM, EPI, RPB, MR>(a, n_blocks, st);
+      case 8192: return launch_layer_gemv<T, 16, NORM, EPI, RPB, MR>(a, n_blocks, st);
+      default: break;
+    }
+  }
+  return hipErrorInvalidValue;
 }
 
 template <typename T, int EPI, int RPB>
@@ -464,8 +499,8 @@ extern "C" int32_t mi_w8a16_linear_fused(
     return MI_ERR_INVALID;
   }
   if (epilogue == kEpiSwiglu && (st = check_w(w_b, s_b, w_sn_b, what)) != MI_OK) return st;
-  if (epilogue == kEpiSwiglu && norm_w != nullptr && K > 4096) {
-    set_last_error("%s: SwiGLU with the RMSNorm prologue supports K <= 4096 (K=%lld)", what,
+  if (epilogue == kEpiSwiglu && K > 4096) {
+    set_last_error("%s: the SwiGLU epilogue supports K <= 4096 (K=%lld)", what,
                    (long long)K);
     return MI_ERR_UNSUPPORTED;
   }

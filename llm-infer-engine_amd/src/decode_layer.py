@@ -47,10 +47,12 @@ def supported(M: int, K: int, dtype: torch.dtype, lin, norm_weight=None, *,
         return False
     if s.dtype != dtype or not s.is_contiguous():
         return False
+    if swiglu and K > 4096:
+        return False
     if norm_weight is not None:
         if (norm_weight.dtype != dtype or not norm_weight.is_contiguous()
                 or norm_weight.data_ptr() % 16 != 0 or M * K * 2 > 64 * 1024
-                or (M > 8 and K > 2048) or (swiglu and K > 4096)):
+                or (M > 8 and K > 2048)):
             return False
     return True
 

@@ -138,6 +138,13 @@ def test_unsupported_shapes_are_rejected(dev):
         decode_layer.linear_fused(x, lin)
     lin2 = _linear(dev, 512, 64, torch.bfloat16, 9)
     assert not decode_layer.supported(17, 512, torch.bfloat16, lin2)
+    # two weight streams (SwiGLU) are built for K <= 4096 only
+    lin3 = _linear(dev, 8192, 64, torch.bfloat16, 9)
+    x3 = randn((4, 8192), 10, torch.bfloat16, dev)
+    assert decode_layer.supported(4, 8192, torch.bfloat16, lin3)
+    assert not decode_layer.supported(4, 8192, torch.bfloat16, lin3, swiglu=True)
+    with pytest.raises(NotImplementedError):
+        decode_layer.linear_fused(x3, lin3, lin_b=lin3)
 
 
 def test_qkv_position_outside_cache_writes_nothing(dev):
