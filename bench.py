@@ -7,9 +7,10 @@ Headline (`value`): BASELINE config 2 — causal GQA prefill, bf16, B4 S2048
 4: B1 L=131072, split sweep) in GB/s, each with its own roofline, and the CPU
 baseline (the fp32 oracle on the host cores, on a bounded sample).
 
-A step is one flash_attention call on resident inputs.  Timing: W untimed
-warm-up steps, then K steps between torch.cuda.synchronize() calls, with HIP
-events (torch's current stream — the stream the kernels are launched on).
+A step is one flash_attention call on resident inputs.  Timing: untimed
+warm-up (at least W steps and at least 0.25 s of back-to-back steps, so the GPU
+clock has settled), then K steps between torch.cuda.synchronize() calls, with
+HIP events (torch's current stream — the stream the kernels are launched on).
 Decode steps are replayed from captured hipGraphs (one per rotating buffer set,
 so the 256 MB MALL cannot serve repeated reads).
 
@@ -58,6 +59,21 @@ def _traffic(summary: str, key: str):
     return None
 
 
+def _settle(torch, fn, warmup: int, min_s: float = 0.25) -> None:
+    """Untimed warm-up: at least `warmup` calls and at least `min_s` seconds of
+    back-to-back work, so the GPU clock has settled before the timed region
+    (a handful of sub-millisecond launches does not get there)."""
+    import time
+    for _ in range(max(warmup, 1)):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < min_s:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
 def bench_prefill(torch, steps: int, warmup: int) -> dict:
     from src.flash_attn import flash_attention
     dev = torch.device("cuda:0")
@@ -69,9 +85,7 @@ def bench_prefill(torch, steps: int, warmup: int) -> dict:
     v = torch.randn((B, Hkv, S, D), generator=g).to(torch.bfloat16).to(dev)
     flops = 4.0 * B * Hq * S * S * D / 2
     step = lambda: flash_attention(q, k, v, sm_scale=1.0, return_lse=True)  # noqa: E731
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    _settle(torch, step, warmup)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record()
@@ -113,9 +127,12 @@ def _graph_decode(torch, fn, n_sets):
 
 
 def _time_graphs(torch, graphs, steps, warmup):
-    for i in range(warmup):
-        graphs[i % len(graphs)].replay()
-    torch.cuda.synchronize()
+    it = [0]
+
+    def replay_next():
+        graphs[it[0] % len(graphs)].replay()
+        it[0] += 1
+    _settle(torch, replay_next, warmup)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record()

@@ -626,9 +626,11 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
         for (int i = 0; i < 16; ++i)
           if (16 * (i >> 3) + (i & 7) > tri) s[rb][i] = -INFINITY;
       }
-      float x = fmaxf(s[rb][0], s[rb][1]);
+      // running max as a chain of 3-input maxima (v_max3_f32: 8 ops per 16)
+      float x = fmaxf(fmaxf(s[rb][0], s[rb][1]), s[rb][2]);
 #pragma unroll
-      for (int i = 2; i < 16; i += 2) x = fmaxf(x, fmaxf(s[rb][i], s[rb][i + 1]));
+      for (int i = 3; i < 15; i += 2) x = fmaxf(fmaxf(x, s[rb][i]), s[rb][i + 1]);
+      x = fmaxf(x, s[rb][15]);
       auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
       mx[rb] = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl2;
     }
@@ -683,6 +685,20 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
   };
   using TT = std::true_type;
   using FF = std::false_type;
+  // Issue order of a steady-state slot: the slot's LDS operand reads first,
+  // then one MFMA followed by a run of softmax VALU work, repeated.  A wave's
+  // own VALU issue stalls for about half of each 32x32x16 MFMA, so spreading
+  // the 16 MFMAs evenly through the ~150 softmax instructions keeps the matrix
+  // pipe fed instead of bunching MFMAs behind the row-max chain.
+  auto interleave = [&]() {
+    __builtin_amdgcn_sched_group_barrier(0x100, 12, 0);   // DS reads
+    __builtin_amdgcn_sched_group_barrier(0x402, 12, 0);   // VALU (incl. exp)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x402, 9, 0);  // VALU
+    }
+  };
   // slot A(t): softmax(t.h0) | PV(t-1.h1), QK(t.h1).  HAS_PV: t > 0;
   // DIAG: t is the wave's diagonal tile (its second half is hidden from rb 0).
   auto slot_a = [&](const unsigned char* cur, const unsigned char* prv, auto has_pv_c, auto diag_c) {
@@ -690,6 +706,7 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
     if constexpr (HAS_PV) pv(prv, 1, pB, TT{});
     qk(cur, 1, sB, std::integral_constant<bool, !DIAG>{});
     const bool resc = smax(sA, pA, TT{}, std::integral_constant<bool, DIAG>{}, FF{});
+    if constexpr (HAS_PV && !DIAG) interleave();
     if (resc) rescale_o(TT{});
   };
   // slot B(t): softmax(t.h1) | PV(t.h0), QK(t+1.h0); on the diagonal tile,
@@ -699,7 +716,9 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
     pv(cur, 0, pA, TT{});
     if constexpr (!DIAG) {
       qk(nxt, 0, sA, TT{});
-      if (smax(sB, pB, TT{}, FF{}, FF{})) rescale_o(TT{});
+      const bool resc = smax(sB, pB, TT{}, FF{}, FF{});
+      interleave();
+      if (resc) rescale_o(TT{});
     } else {
       if (smax(sB, pB, FF{}, FF{}, TT{})) rescale_o(FF{});
       pv(cur, 1, pB, FF{});
