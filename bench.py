@@ -11,8 +11,9 @@ A step is one flash_attention call on resident inputs.  Timing: untimed
 warm-up (at least W steps and at least 0.25 s of back-to-back steps, so the GPU
 clock has settled), then K steps between torch.cuda.synchronize() calls, with
 HIP events (torch's current stream — the stream the kernels are launched on).
-Decode steps are replayed from captured hipGraphs (one per rotating buffer set,
-so the 256 MB MALL cannot serve repeated reads).
+Decode calls are replayed from a captured hipGraph holding one call per
+rotating buffer set (consecutive calls in one graph, like a captured decode
+loop; the sets are large enough that the 256 MB MALL cannot serve re-reads).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 """
@@ -110,7 +111,8 @@ def bench_prefill(torch, steps: int, warmup: int) -> dict:
 
 
 def _graph_decode(torch, fn, n_sets):
-    graphs = []
+    """One hipGraph holding n_sets consecutive decode calls, one per rotating
+    buffer set (a captured decode loop: consecutive calls share one launch)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -118,29 +120,26 @@ def _graph_decode(torch, fn, n_sets):
             fn(i)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    for i in range(n_sets):
-        gr = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gr):
+    gr = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gr):
+        for i in range(n_sets):
             fn(i)
-        graphs.append(gr)
-    return graphs
+    return gr
 
 
-def _time_graphs(torch, graphs, steps, warmup):
-    it = [0]
-
-    def replay_next():
-        graphs[it[0] % len(graphs)].replay()
-        it[0] += 1
-    _settle(torch, replay_next, warmup)
+def _time_graph(torch, graph, calls, steps, warmup):
+    """ms per call: replays of `graph` (holding `calls` calls) covering at
+    least `steps` calls, after a settled warm-up."""
+    replays = max(1, -(-steps // calls))
+    _settle(torch, graph.replay, max(1, -(-warmup // calls)))
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record()
-    for i in range(steps):
-        graphs[i % len(graphs)].replay()
+    for _ in range(replays):
+        graph.replay()
     ev1.record()
     torch.cuda.synchronize()
-    return ev0.elapsed_time(ev1) / steps
+    return ev0.elapsed_time(ev1) / (replays * calls)
 
 
 def bench_decode_cfg3(torch, steps: int, warmup: int) -> dict:
@@ -156,8 +155,8 @@ def bench_decode_cfg3(torch, steps: int, warmup: int) -> dict:
         vs.append(torch.randn((16, 8, 8192, 128), generator=g).to(torch.bfloat16).to(dev))
     sl = lens.to(dev)
     nbytes = int(lens.sum()) * 8 * 128 * 2 * 2 + 2 * 16 * 24 * 128 * 2
-    graphs = _graph_decode(torch, lambda i: flash_decode(qs[i], ks[i], vs[i], seq_lens=sl), n_sets)
-    ms = _time_graphs(torch, graphs, max(steps, 20), warmup)
+    graph = _graph_decode(torch, lambda i: flash_decode(qs[i], ks[i], vs[i], seq_lens=sl), n_sets)
+    ms = _time_graph(torch, graph, n_sets, max(steps, 21), warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
     out = {
         "config": "3: decode B16 24/8 D128 T8192 L~U[1024,8192] (sum 96634), seq_lens, hipGraph",
@@ -167,7 +166,7 @@ def bench_decode_cfg3(torch, steps: int, warmup: int) -> dict:
                      "traffic": _traffic("decode_config3_4_traffic.md",
                                          "hbm_bytes_per_launch_config3")},
     }
-    del graphs, ks, vs
+    del graph, ks, vs
     torch.cuda.empty_cache()
     return out
 
@@ -183,11 +182,11 @@ def bench_decode_cfg4(torch, steps: int, warmup: int) -> dict:
     nbytes = 131072 * 8 * 128 * 2 * 2 + 2 * 24 * 128 * 2
     sweep = {}
     for splits in (16, 32, 64, 128):
-        graphs = _graph_decode(
+        graph = _graph_decode(
             torch, lambda i, s=splits: flash_decode(qs[i], ks[i], vs[i], num_splits=s), n_sets)
-        ms = _time_graphs(torch, graphs, max(steps, 20), warmup)
+        ms = _time_graph(torch, graph, n_sets, max(steps, 20), warmup)
         sweep[str(splits)] = round(nbytes / (ms * 1e-3) / 1e9, 1)
-        del graphs
+        del graph
     best = max(sweep.values())
     out = {"config": "4: decode B1 L131072 24/8 D128, splits sweep (combine included)",
            "unit": "GB/s", "by_splits": sweep, "value": best,
@@ -216,7 +215,7 @@ def bench_config5(torch, steps: int, warmup: int) -> dict:
     kv.v[:, :, :, :4096].normal_(generator=g)
     tok = torch.randint(0, args.vocab_size, (8, 1), generator=torch.Generator().manual_seed(0)).to(dev)
     runner.set_inputs(tok, 4096)
-    ms = _time_graphs(torch, [runner.graph], max(steps, 20), warmup)
+    ms = _time_graph(torch, runner.graph, 1, max(steps, 20), warmup)
     # int8 linears + bf16 lm_head + K/V read (4097 slots) + scales, per step
     D, L = 64, 16
     lin = L * (2048 * 2048 * 2 + 2 * 512 * 2048 + 3 * 2048 * 8192)

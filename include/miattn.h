@@ -262,6 +262,31 @@ int32_t mi_w8a16_qkv_rope_append(
     int64_t capacity, int64_t m, int64_t k, int64_t n_heads, int64_t n_kv_heads,
     int64_t head_dim, int32_t dtype, void* stream);
 
+/*
+ * Decode-step output projection (lm_head), 1 <= m <= 16 rows, k % 512 == 0,
+ * k <= 4096, bf16/fp16:
+ *   a        = rmsnorm(x, norm_w, eps) if norm_w != NULL else x  (rounded to dtype)
+ *   y[m, n]  = dtype(sum_k a[m, k] * w[n, k])                    (fp32 accumulate)
+ *   argmax_out[m] = first n with y[m, n] == max_n y[m, n]   (if argmax_out != NULL)
+ * x [m, k] (row stride x_sm), w [n, k] in x's dtype (row stride w_sn), y [m, n]
+ * (row stride y_sm); x/w/norm_w rows 16-byte aligned.  The
+ * argmax needs fp32 part_v and int32 part_i workspaces of n_parts >=
+ * mi_lm_head_partials(m, n) entries per row (row stride n_parts); NaN logits
+ * are not ranked.  Two launches with argmax, one without.
+ * Replaces, fused: the final norm + output Linear  src/model.py:137,183
+ * (RMSNorm src/rms_norm.py:32-38) and greedy sampling's torch.argmax
+ * src/sampler.py:30 (the per-token host sync of main.py:260 becomes a device
+ * tensor).
+ */
+int32_t mi_lm_head(const void* x, int64_t x_sm, const void* norm_w, float eps,
+                   const void* w, int64_t w_sn, void* y, int64_t y_sm,
+                   int64_t* argmax_out, float* part_v, int32_t* part_i,
+                   int64_t n_parts, int64_t m, int64_t n, int64_t k, int32_t dtype,
+                   void* stream);
+
+/* Partial-buffer entries per row that mi_lm_head's argmax needs (0 if m or n <= 0). */
+int64_t mi_lm_head_partials(int64_t m, int64_t n);
+
 #ifdef __cplusplus
 }
 #endif

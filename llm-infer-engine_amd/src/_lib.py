@@ -126,6 +126,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i64, _i64, _i64, _i64, _i64,          # M K n_heads n_kv_heads head_dim
         _i32, _ptr,                            # dtype stream
     ]),
+    "mi_lm_head": (_i32, [
+        _ptr, _i64, _ptr, _f32,                # x x_sm norm_w eps
+        _ptr, _i64, _ptr, _i64,                # w w_sn y y_sm
+        _ptr, _ptr, _ptr, _i64,                # argmax_out part_v part_i n_parts
+        _i64, _i64, _i64, _i32, _ptr,          # m n k dtype stream
+    ]),
+    "mi_lm_head_partials": (_i64, [_i64, _i64]),
 }
 
 _lock = threading.Lock()

@@ -12,7 +12,10 @@ MI355X version changes:
     are gathered on the device from the model's resident cos/sin table (the
     reference copies a freqs row from the CPU table every step, :64);
   * attention reads exactly pos+1 keys per row through ``seq_lens`` instead of
-    scanning all max_seq_len slots behind a rewritten bool mask (:65-66).
+    scanning all max_seq_len slots behind a rewritten bool mask (:65-66);
+  * ``greedy=True`` also captures the greedy argmax of the logits
+    (``decode_greedy`` returns the next tokens as a device tensor), so a
+    greedy token loop never waits on the host (main.py:259-260 syncs per token).
 All launches inside the graph are the HIP kernels of libmiattn.so plus the
 library GEMMs/elementwise ops of the model.
 """
@@ -27,7 +30,7 @@ from .kv_cache import KVCache
 
 class CUDAGraphDecodeRunner:
     def __init__(self, model: nn.Module, model_args: ModelArgs, kv_cache: KVCache, device: str,
-                 *, batch_size: int | None = None):
+                 *, batch_size: int | None = None, greedy: bool = False):
         if not str(device).startswith("cuda"):
             raise ValueError("CUDAGraphDecodeRunner requires CUDA device")
         self.model = model
@@ -44,12 +47,18 @@ class CUDAGraphDecodeRunner:
         self.static_scatter_positions = torch.zeros((1,), dtype=torch.long, device=device)
         self.static_seq_lens = torch.ones((B,), dtype=torch.long, device=device)
         self.static_logits = None
+        self.static_tokens = None
+        self.greedy = bool(greedy)
         self._capture()
 
     def _forward(self):
-        return self.model(self.static_input_token, kv_cache=self.kv_cache, use_cuda_graph=True,
-                          scatter_positions=self.static_scatter_positions,
-                          seq_lens=self.static_seq_lens)
+        out = self.model(self.static_input_token, kv_cache=self.kv_cache, use_cuda_graph=True,
+                         scatter_positions=self.static_scatter_positions,
+                         seq_lens=self.static_seq_lens, greedy=self.greedy)
+        if self.greedy:
+            logits, self.static_tokens = out
+            return logits
+        return out
 
     def _capture(self):
         torch.cuda.nvtx.range_push("CUDAGraphWarmup")
@@ -84,3 +93,12 @@ class CUDAGraphDecodeRunner:
         self.graph.replay()
         torch.cuda.nvtx.range_pop()
         return self.static_logits
+
+    def decode_greedy(self, token_id, current_pos: int) -> torch.Tensor:
+        """One step and its greedy next tokens [B, 1] (device int64, no host
+        sync).  Requires the runner to be built with ``greedy=True``; the
+        returned tensor can be passed straight back as the next ``token_id``."""
+        if not self.greedy:
+            raise ValueError("decode_greedy needs CUDAGraphDecodeRunner(..., greedy=True)")
+        self.decode(token_id, current_pos)
+        return self.static_tokens

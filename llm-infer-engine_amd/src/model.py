@@ -13,12 +13,17 @@ Extensions (keyword-only, defaults keep the reference behaviour):
   * in graph mode (use_cuda_graph=True with scatter_positions and no explicit
     freqs_cis) cos/sin come from the model's device-resident table indexed by
     the device position, so a replay copies nothing from the host.
+  * ``greedy=True`` returns (logits, tokens): tokens [B, 1] int64 is the
+    argmax of the returned logits, computed on the device.
+The final norm and the output projection of up to 16 rows (decode, or the
+last position of a prefill) run as one fused launch (src/lm_head.py).
 """
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
 
+from . import lm_head
 from .flash_attn import flash_attention
 from .flash_decode import flash_decode
 from .rms_norm import RMSNorm
@@ -148,7 +153,7 @@ class Llama3(nn.Module):
 
     def forward(self, tokens, start_pos=0, kv_cache=None, freqs_cis=None, use_cuda_graph=False,
                 scatter_positions=None, decode_attn_mask=None, return_all_logits=False, *,
-                seq_lens=None):
+                seq_lens=None, greedy=False):
         torch.cuda.nvtx.range_push("Embed")
         h = self.tok_embeddings(tokens)
         torch.cuda.nvtx.range_pop()
@@ -172,6 +177,14 @@ class Llama3(nn.Module):
         torch.cuda.nvtx.range_push("Output")
         if not return_all_logits and seq_len > 1:
             h = h[:, -1:, :]
-        out = self.output(self.norm(h))
+        rows = h.shape[0] * h.shape[1]
+        if h.is_cuda and lm_head.supported(rows, h.shape[-1], self.output.weight, self.norm.weight):
+            # final norm + output projection (+ greedy argmax) in one launch
+            out = lm_head.lm_head(h, self.output.weight, self.norm.weight, self.norm.eps,
+                                  greedy=greedy)
+        else:
+            out = self.output(self.norm(h))
+            if greedy:
+                out = (out, torch.argmax(out, dim=-1))
         torch.cuda.nvtx.range_pop()
         return out
