@@ -86,3 +86,41 @@ def test_rope_kv_append_rejects_out_of_capacity():
                                60, None, 1, 8, 10, 64, 64,
                                *([1] * 16), 1, 1, 1, 1, 0, 0, 0, None)
     assert st == -1 and "capacity" in _lib.last_error()
+
+
+def _lm_head_call(lib, **over):
+    a = dict(x=1 << 20, x_sm=2048, norm=None, eps=1e-5, w=1 << 21, w_sn=2048, y=1 << 22,
+             y_sm=1000, tok=None, pv=None, pi=None, n_parts=0, m=8, n=1000, k=2048, dtype=0)
+    a.update(over)
+    return lib.mi_lm_head(a["x"], a["x_sm"], a["norm"], a["eps"], a["w"], a["w_sn"], a["y"],
+                          a["y_sm"], a["tok"], a["pv"], a["pi"], a["n_parts"], a["m"], a["n"],
+                          a["k"], a["dtype"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    ({"x": None}, -1, "null"),
+    ({"m": 0}, -1, "positive"),
+    ({"dtype": 2}, -2, "dtype"),
+    ({"m": 17}, -2, "unsupported"),
+    ({"k": 1000, "x_sm": 1000, "w_sn": 1000}, -2, "unsupported"),
+    ({"x": (1 << 20) + 8}, -1, "aligned"),
+    ({"w_sn": 2040}, -1, "aligned"),
+])
+def test_lm_head_c_side_validation(over, code, msg):
+    """mi_lm_head rejects bad calls before touching the device."""
+    from src import _lib
+    lib = _lib.load()
+    assert _lm_head_call(lib, **over) == code
+    assert msg in _lib.last_error()
+    assert lib.mi_lm_head_partials(0, 1000) == 0
+
+
+def test_lm_head_python_rules_without_gpu():
+    import torch
+    from src import lm_head as lh
+    w = torch.zeros(64, 512, dtype=torch.bfloat16)
+    assert not lh.supported(4, 512, w)             # host tensor
+    with pytest.raises(TypeError, match="dtype"):
+        lh.lm_head(torch.zeros(4, 512, dtype=torch.float16), w)
+    with pytest.raises(ValueError, match="CUDA"):
+        lh.lm_head(torch.zeros(4, 512, dtype=torch.bfloat16), w)
