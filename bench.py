@@ -4,8 +4,10 @@ Headline (`value`): BASELINE config 2 — causal GQA prefill, bf16, B4 S2048
 32/8 heads D64, fp32 LSE output, in TFLOP/s of algorithmic work
 (4*B*Hq*S^2*D/2 = 68.72 GFLOP per step).  The same line carries, under
 `extra`, the HBM-bound decode configs (3: B16 24/8 D128 T8192 ragged lengths;
-4: B1 L=131072, split sweep) in GB/s, each with its own roofline, and the CPU
-baseline (the fp32 oracle on the host cores, on a bounded sample).
+4: B1 L=131072, split sweep) in GB/s, the W8A16 decode step (config 5) in
+tokens/s, and the W8A16 prefill GEMM (one layer's projections at config 2's
+8192 tokens) in TFLOP/s, each with its own roofline; and the CPU baseline (the
+fp32 oracle on the host cores, on a bounded sample).
 
 A step is one flash_attention call on resident inputs.  Timing: untimed
 warm-up (at least W steps and at least 0.25 s of back-to-back steps, so the GPU
@@ -233,6 +235,66 @@ def bench_config5(torch, steps: int, warmup: int) -> dict:
     return out
 
 
+def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
+    """The seven W8A16 projections of one Llama-3.2-1B layer at config 2's token
+    count (M = 4 x 2048), one mi_w8a16_gemm call each, back to back."""
+    from src import _lib
+    dev = torch.device("cuda:0")
+    lib = _lib.load()
+    M = 4 * 2048
+    shapes = [("wq", 2048, 2048), ("wk", 512, 2048), ("wv", 512, 2048), ("wo", 2048, 2048),
+              ("w1", 8192, 2048), ("w3", 8192, 2048), ("w2", 2048, 8192)]   # (name, N, K)
+    g = torch.Generator("cpu").manual_seed(0)
+    xs = {K: torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev) for K in (2048, 8192)}
+    ws = [torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev) for _, N, K in shapes]
+    ss = [(torch.rand(N, generator=g) * 0.02 + 1e-3).to(torch.bfloat16).to(dev) for _, N, _ in shapes]
+    ys = [torch.empty(M, N, device=dev, dtype=torch.bfloat16) for _, N, _ in shapes]
+    stream = _lib.stream_of(xs[2048])
+
+    def call(i):
+        _, N, K = shapes[i]
+        x = xs[K]
+        st = lib.mi_w8a16_gemm(x.data_ptr(), ws[i].data_ptr(), ss[i].data_ptr(), ys[i].data_ptr(),
+                               M, N, K, K, K, 1, N, 0, 0, stream)
+        _lib.check(st, "w8a16_gemm")
+
+    def step():
+        for i in range(len(shapes)):
+            call(i)
+
+    def timed(fn, n):
+        _settle(torch, fn, warmup)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    ms = timed(step, steps)
+    flops = sum(2.0 * M * N * K for _, N, K in shapes)
+    per = {}
+    for i, (name, N, K) in enumerate(shapes):
+        t = timed(lambda: call(i), steps)
+        per[name] = {"N": N, "K": K, "us": round(t * 1e3, 2),
+                     "tflops": round(2.0 * M * N * K / (t * 1e-3) / 1e12, 1)}
+    tf = flops / (ms * 1e-3) / 1e12
+    # the dominant shape (w1/w3: 2 of the 7 calls, 54 % of the flops)
+    dom = per["w1"]
+    out = {"config": "W8A16 prefill projections of one Llama-3.2-1B layer, M = 8192 tokens "
+                     "(config 2's B4 x S2048), bf16 activations, int8 weights, bf16 scales",
+           "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
+           "flops_per_step": flops, "per_projection": per,
+           "roofline": {"bound": "mfma", "kernel": "w8a16_gemm_kernel (w1 shape)",
+                        "achieved": dom["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(dom["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": None}}
+    del xs, ws, ss, ys
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(torch) -> dict:
     """The fp32 CPU oracle on batch 0 of config 2 (1/4 of a step), on rank 0."""
     from oracle import attention as ora
@@ -266,7 +328,7 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one plain 1 GiB device copy (scales rocprofv3 FETCH/WRITE_SIZE)")
-    ap.add_argument("--only", choices=["prefill", "decode", "step"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "step", "gemm"], default=None,
                     help="run one leg only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -296,6 +358,8 @@ def main() -> None:
         extra["decode_config4"] = bench_decode_cfg4(torch, args.steps, args.warmup)
     if args.only in (None, "step"):
         extra["decode_step_config5"] = bench_config5(torch, args.steps, args.warmup)
+    if args.only in (None, "gemm"):
+        extra["w8a16_prefill_gemm"] = bench_w8a16_prefill(torch, args.steps, args.warmup)
     cpu = None
     if not args.no_cpu_baseline and args.only is None:
         cpu = cpu_baseline(torch)

@@ -214,6 +214,20 @@ int32_t mi_w8a16_gemv(const void* x, const int8_t* w, const void* scales,
                       void* stream);
 
 /*
+ * W8A16 GEMM for prefill-sized inputs (any m >= 1):
+ * y[m, n] = (sum_k x[m,k] * w[n,k]) * scales[n], int8 widened exactly to x's
+ * dtype, fp32 accumulate on MFMA, y in x's dtype (bf16/fp16).  x rows
+ * (unit k stride, row stride x_sm elements) and w rows (w_sn bytes) 16-byte
+ * aligned; k % 64 == 0; y has unit column stride and row stride y_sm.
+ * Replaces w8a16_gemm_kernel + w8a16_gemm_launch
+ *   src/quant_linear.py:123-188, src/quant_linear.py:191-247.
+ */
+int32_t mi_w8a16_gemm(const void* x, const int8_t* w, const void* scales,
+                      void* y, int64_t m, int64_t n, int64_t k, int64_t x_sm,
+                      int64_t w_sn, int64_t s_sn, int64_t y_sm, int32_t dtype,
+                      int32_t sdtype, void* stream);
+
+/*
  * Fused decode-step projection (1 <= m <= 16 rows; k one of 512, 1024, 1536,
  * 2048, 3072, 4096, 6144, 8192):
  *   a   = rmsnorm(x, norm_w, eps) if norm_w != NULL else x   (rounded to dtype)

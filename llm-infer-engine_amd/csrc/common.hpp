@@ -129,4 +129,29 @@ __device__ inline u32x4 load16_stream(const void* p) {
   return __builtin_nontemporal_load(q);
 }
 
+// ------------------------------------------------- LDS tile staging
+// One wave-wide 16-byte-per-lane global->LDS copy: lane t's 16 bytes at
+// base + voff land at LDS byte address lds + 16 t.  Issued as inline asm on
+// purpose: the compiler does not track it, so it does not insert a wait for
+// the copy before unrelated LDS reads of the other buffer; completion is
+// awaited explicitly (dma_wait_all) before the barrier that publishes the tile.
+// The compiler's hazard recognizer does not look inside inline asm, so the asm
+// supplies the wait states itself: s_nop 4 (5 wait states) covers both a VALU
+// write of the base SGPRs (v_readlane / v_readfirstlane, 5 required before a
+// VMEM read) and the M0 write (1 required before an LDS DMA).
+__device__ inline void lds_dma16(const unsigned char* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(lds)
+               : "memory");
+}
+__device__ inline uint32_t lds_addr(const unsigned char* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) unsigned char*)(p);
+}
+__device__ inline void dma_wait_all() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ inline void block_sync_lds() {
+  // LDS reads of this wave are complete and every wave has arrived; the
+  // tile copies (vmcnt) are waited for separately where a tile is published.
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 }  // namespace mi

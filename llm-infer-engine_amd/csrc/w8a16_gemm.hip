@@ -1,0 +1,334 @@
+// W8A16 GEMM for prefill: y[m, n] = (sum_k x[m, k] * q[n, k]) * s[n], any M.
+//
+// Math of the reference's GEMM kernel (src/quant_linear.py:123-188): the int8
+// weight is converted to the activation dtype (exact, |q| <= 128), products are
+// accumulated in fp32, the per-row scale is applied once to the finished sum
+// (:180-183) and the result is rounded to x's dtype.  The reference dispatches
+// to it when the flattened input has more than 8 rows (:273).
+//
+// MI355X design.  At prefill sizes (M in the thousands) the product is
+// MFMA-bound: a 128 x 256 (m x n) output tile per workgroup of 4 waves, 64-deep
+// k stages, v_mfma_f32_32x32x16_{bf16,f16} with fp32 accumulators, two
+// workgroups per CU (two waves per SIMD, so one wave's VALU and LDS work issues
+// under the other's MFMAs).
+//  * Each wave owns 64 output columns (n) and all 128 rows (m).  The activation
+//    tile is shared by the 4 waves and copied global->LDS by DMA
+//    (global_load_lds_dwordx4: no VGPRs, no VALU); the int8 weight fragments
+//    are private to a wave and go straight from global memory to registers
+//    (a wave's 64 rows x 64 k = 4 KB per stage).  Both are fetched one stage
+//    ahead.
+//  * The weight is widened to the activation dtype in registers right before
+//    the MFMAs; every widened fragment feeds 4 MFMAs: 1.5 VALU ops per element
+//    = 3 per 32x32x16 MFMA.
+//  * The weight rows are the MFMA A operand and the activation rows the B
+//    operand, so each lane's accumulators hold 4 consecutive output columns
+//    of one row (8-byte stores).
+//  * The k order inside a 64-deep stage is permuted identically for both
+//    operands: the lane of half h feeds k = 32h + 8j .. 32h + 8j + 7 to MFMA
+//    step j, so it reads 32 contiguous k of a row (two 16-byte loads of the
+//    weight row, four 16-byte LDS reads of the activation row).  The sum is
+//    over the same k.
+//  * Activation rows are XOR-swizzled by 16-byte chunk in LDS so those reads
+//    are free of bank conflicts; the DMA realises the swizzle by choosing which
+//    chunk each lane fetches (a DMA wave instruction writes 1 KB contiguously).
+//  * The 256 column scales are staged in LDS at the start, so the epilogue has
+//    no dependent global loads.
+//  * Tiles are ordered so that concurrently resident workgroups of one XCD
+//    (blocks are dealt to the 8 XCDs round-robin) cover a patch of 8 m-tiles
+//    and share their operand rows in that XCD's L2.
+#include "common.hpp"
+
+namespace mi {
+
+struct GemmArgs {
+  const unsigned char* x;  // [M, K] activations (unit k stride), rows x_sm elements apart
+  const unsigned char* w;  // [N, K] int8, rows w_sn bytes apart
+  const void* scales;      // [N] (element stride s_sn)
+  void* y;                 // [M, N] (unit n stride), rows y_sm elements apart
+  int64_t x_sm, w_sn, s_sn, y_sm;
+  int32_t M, N, K;
+  int32_t tiles_m, tiles_n;
+  int32_t y_vec;           // rows of y allow 8-byte stores of 4 columns
+};
+
+constexpr int kGmBM = 128;                      // output rows (m) per workgroup
+constexpr int kGmBN = 256;                      // output columns (n) per workgroup
+constexpr int kGmBK = 64;                       // k per stage
+constexpr int kGmXBytes = kGmBM * kGmBK * 2;    // activation tile per stage, 16 KB
+constexpr int kGmXDma = kGmXBytes / 1024 / 4;   // 1 KB DMA instructions per wave and stage
+constexpr int kGmGroupM = 8;                    // m-tiles per tile group
+// LDS: two activation stages, then the workgroup's column scales (fp32)
+constexpr size_t kGmLdsBytes = 2 * kGmXBytes + kGmBN * sizeof(float);
+
+// chunk swizzle of activation row r (8 chunks of 16 bytes per row)
+__device__ inline int gm_xswz(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
+
+template <typename T> struct GemmOps;
+template <> struct GemmOps<bf16_t> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  __device__ static inline f32x16 mma(const v8& a, const v8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  // upper halves of two fp32 values whose low 16 bits are zero
+  __device__ static inline uint32_t hi2(float lo, float hi) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+  }
+  // 8 int8 (two words) -> 8 bf16, exact: each byte is sign-extended and
+  // converted to fp32 (one SDWA op); integers of magnitude <= 128 have 8
+  // significant bits, so the fp32 upper halves are the bf16 values.
+  __device__ static inline v8 widen(uint32_t lo, uint32_t hi) {
+    u32x4 r;
+    r.x = hi2((float)(int8_t)lo, (float)(int8_t)(lo >> 8));
+    r.y = hi2((float)(int8_t)(lo >> 16), (float)(int8_t)(lo >> 24));
+    r.z = hi2((float)(int8_t)hi, (float)(int8_t)(hi >> 8));
+    r.w = hi2((float)(int8_t)(hi >> 16), (float)(int8_t)(hi >> 24));
+    return __builtin_bit_cast(v8, r);
+  }
+};
+template <> struct GemmOps<f16_t> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  __device__ static inline f32x16 mma(const v8& a, const v8& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  // two bytes of u (= q ^ 0x80 = q + 128) -> fp16 pair 1024 + u (bit pattern
+  // 0x6400 | u), minus 1152 -> q exactly (fp16 spacing is 1 in [1024, 2048)).
+  __device__ static inline uint32_t pair(uint32_t u, uint32_t sel) {
+    const h2 v = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, sel));
+    return __builtin_bit_cast(uint32_t, v - h2{(_Float16)1152.f, (_Float16)1152.f});
+  }
+  __device__ static inline v8 widen(uint32_t lo, uint32_t hi) {
+    lo ^= 0x80808080u;
+    hi ^= 0x80808080u;
+    u32x4 r;
+    r.x = pair(lo, 0x04010400u);
+    r.y = pair(lo, 0x04030402u);
+    r.z = pair(hi, 0x04010400u);
+    r.w = pair(hi, 0x04030402u);
+    return __builtin_bit_cast(v8, r);
+  }
+};
+
+// Tile of a linear workgroup id: ids dealt round-robin to the 8 XCDs are first
+// regrouped so that each XCD's ids are consecutive, then consecutive ids walk
+// groups of kGmGroupM m-tiles, m fastest.
+__device__ inline void gm_tile(const GemmArgs& a, int& tm, int& tn) {
+  const int G = a.tiles_m * a.tiles_n;
+  int b = blockIdx.x;
+  if ((G & 7) == 0) b = (b & 7) * (G >> 3) + (b >> 3);
+  const int group = kGmGroupM * a.tiles_n;
+  const int g = b / group, first = g * kGmGroupM;
+  const int gm = min(a.tiles_m - first, kGmGroupM);
+  const int in = b - g * group;
+  tm = first + in % gm;
+  tn = in / gm;
+}
+
+template <typename T, typename ST>
+__global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
+  using OP = GemmOps<T>;
+  typedef typename OP::v8 v8;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the wave's 64 columns
+  const int r = lane & 31, h = lane >> 5;
+  int tm, tn;
+  gm_tile(a, tm, tn);
+  const int m0 = tm * kGmBM, n0 = tn * kGmBN;
+
+  // the workgroup's 256 column scales as fp32 (read by the epilogue; published
+  // by the main loop's first barrier)
+  float* const sc_lds = reinterpret_cast<float*>(smem_raw + 2 * kGmXBytes);
+  sc_lds[threadIdx.x] = Elem<ST>::to_f32(
+      reinterpret_cast<const ST*>(a.scales)[(int64_t)min(n0 + (int)threadIdx.x, a.N - 1) * a.s_sn]);
+
+  // ---- activation DMA: instruction i of wave wv copies tile rows
+  // 8 (4 wv + i) .. + 8; lane t fetches logical chunk (t % 8) ^ swz(row) of
+  // row t / 8 (byte offsets relative to the stage's first column).
+  uint32_t x_off[kGmXDma];
+#pragma unroll
+  for (int i = 0; i < kGmXDma; ++i) {
+    const int row = 8 * (kGmXDma * wv + i) + (lane >> 3);
+    const int c = (lane & 7) ^ gm_xswz(row);
+    const int gm = min(m0 + row, a.M - 1);                 // rows past M: clamped, never stored
+    x_off[i] = (uint32_t)((int64_t)(gm - m0) * a.x_sm * 2 + c * 16);
+  }
+  const unsigned char* x_base = a.x + (int64_t)m0 * a.x_sm * 2;
+  const uint32_t lds0 = lds_addr(smem_raw);
+  const int nk = a.K / kGmBK;
+  auto issue_x = [&](int s) {
+    const uint32_t xl = lds0 + (s & 1) * kGmXBytes;
+    const unsigned char* xb = x_base + (int64_t)s * kGmBK * 2;
+#pragma unroll
+    for (int i = 0; i < kGmXDma; ++i) lds_dma16(xb, x_off[i], xl + (kGmXDma * wv + i) * 1024);
+  };
+
+  // ---- weight fragments: lane (r, h) of fragment nf loads the 32 k
+  // 32h .. 32h + 31 of the stage from weight row n0 + 64 wv + 32 nf + r (rows
+  // past N clamped, never stored).
+  const unsigned char* w_row[2];
+#pragma unroll
+  for (int nf = 0; nf < 2; ++nf)
+    w_row[nf] = a.w + (int64_t)min(n0 + 64 * wv + 32 * nf + r, a.N - 1) * a.w_sn + 32 * h;
+  auto load_w = [&](int s, u32x4 (&q)[2][2]) {
+#pragma unroll
+    for (int nf = 0; nf < 2; ++nf)
+#pragma unroll
+      for (int e = 0; e < 2; ++e) q[nf][e] = load16(w_row[nf] + (int64_t)s * kGmBK + 16 * e);
+  };
+
+  // ---- activation fragment mf: LDS row 32 mf + r, chunks 4h + j (j = MFMA k step)
+  int x_rd[4][4];
+#pragma unroll
+  for (int mf = 0; mf < 4; ++mf) {
+    const int row = 32 * mf + r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x_rd[mf][j] = row * 128 + 16 * ((4 * h + j) ^ gm_xswz(row));
+  }
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int mf = 0; mf < 4; ++mf)
+#pragma unroll
+    for (int nf = 0; nf < 2; ++nf)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[mf][nf][i] = 0.f;
+
+  // One stage: stage s's activation tile is in LDS slot s % 2 and its weight
+  // fragments in wc; the copies of stage s + 1 (activation DMA, weight loads
+  // into wn) are issued before its MFMAs so that they land under them.
+  auto step = [&](int s, u32x4 (&wc)[2][2], u32x4 (&wn)[2][2]) {
+    dma_wait_all();                          // this wave's copies of stage s landed
+    // wc is read here, after the wait, so the compiler's own wait for the
+    // weight loads also falls here and not after the next stage's copies
+    __asm__ volatile("" ::"v"(wc[0][0]), "v"(wc[0][1]), "v"(wc[1][0]), "v"(wc[1][1]));
+    // every wave's part of stage s is in LDS, and every wave is done reading
+    // the slot that the next copy overwrites (stage s - 1's)
+    block_sync_lds();
+    if (s + 1 < nk) {
+      issue_x(s + 1);
+      load_w(s + 1, wn);
+    }
+    // keep the next stage's loads ahead of this stage's MFMAs
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned char* st = smem_raw + (s & 1) * kGmXBytes;
+    v8 xa[4][4];
+#pragma unroll
+    for (int mf = 0; mf < 4; ++mf)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        xa[mf][j] = __builtin_bit_cast(v8, *reinterpret_cast<const u32x4*>(st + x_rd[mf][j]));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+      for (int nf = 0; nf < 2; ++nf) {
+        const u32x4& q = wc[nf][j >> 1];
+        const v8 wb = (j & 1) ? OP::widen(q.z, q.w) : OP::widen(q.x, q.y);
+#pragma unroll
+        for (int mf = 0; mf < 4; ++mf) acc[mf][nf] = OP::mma(wb, xa[mf][j], acc[mf][nf]);
+      }
+    }
+  };
+
+  // two register sets for the weight fragments, alternating by stage
+  u32x4 wa[2][2], wb[2][2];
+  issue_x(0);
+  load_w(0, wa);
+  int s = 0;
+  for (; s + 1 < nk; s += 2) {
+    step(s, wa, wb);
+    step(s + 1, wb, wa);
+  }
+  if (s < nk) step(s, wa, wb);
+
+  // ---- epilogue: acc[mf][nf][4 g + i] = C[n][m] with
+  // n = n0 + 64 wv + 32 nf + 8 g + 4 h + i, m = m0 + 32 mf + r
+  T* y = reinterpret_cast<T*>(a.y);
+#pragma unroll
+  for (int nf = 0; nf < 2; ++nf) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int nl = 64 * wv + 32 * nf + 8 * g + 4 * h, nb = n0 + nl;
+      const f32x4 s4 = *reinterpret_cast<const f32x4*>(sc_lds + nl);
+#pragma unroll
+      for (int mf = 0; mf < 4; ++mf) {
+        const int m = m0 + 32 * mf + r;
+        if (m >= a.M) continue;
+        T* yp = y + (int64_t)m * a.y_sm + nb;
+        if (a.y_vec && nb + 3 < a.N) {
+          typedef T t4 __attribute__((ext_vector_type(4)));
+          t4 v;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = Elem<T>::from_f32(acc[mf][nf][4 * g + i] * s4[i]);
+          *reinterpret_cast<t4*>(yp) = v;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (nb + i < a.N) yp[i] = Elem<T>::from_f32(acc[mf][nf][4 * g + i] * s4[i]);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace mi
+
+using namespace mi;
+
+extern "C" int32_t mi_w8a16_gemm(const void* x, const int8_t* w, const void* scales, void* y,
+                                 int64_t m, int64_t n, int64_t k, int64_t x_sm, int64_t w_sn,
+                                 int64_t s_sn, int64_t y_sm, int32_t dtype, int32_t sdtype,
+                                 void* stream) {
+  if (x == nullptr || w == nullptr || scales == nullptr || y == nullptr) {
+    set_last_error("w8a16_gemm: null pointer");
+    return MI_ERR_INVALID;
+  }
+  if (m <= 0 || n <= 0 || k <= 0 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) {
+    set_last_error("w8a16_gemm: need positive M, N, K below 2^31 (M=%lld N=%lld K=%lld)",
+                   (long long)m, (long long)n, (long long)k);
+    return MI_ERR_INVALID;
+  }
+  if (k % kGmBK != 0) {
+    set_last_error("w8a16_gemm: K must be a multiple of %d (K=%lld)", kGmBK, (long long)k);
+    return MI_ERR_UNSUPPORTED;
+  }
+  // tile-relative DMA offsets are 32-bit: 128 activation rows of x_sm elements
+  if (x_sm < k || w_sn < k || y_sm < n || x_sm > (1LL << 23) || w_sn > (1LL << 23)) {
+    set_last_error("w8a16_gemm: row strides must cover a row and be below 2^23 elements");
+    return MI_ERR_INVALID;
+  }
+  if ((uintptr_t)x % 16 != 0 || (x_sm * 2) % 16 != 0 || (uintptr_t)w % 16 != 0 || w_sn % 16 != 0) {
+    set_last_error("w8a16_gemm: x and weight rows must be 16-byte aligned");
+    return MI_ERR_INVALID;
+  }
+  const int64_t tiles_m = (m + kGmBM - 1) / kGmBM, tiles_n = (n + kGmBN - 1) / kGmBN;
+  if (tiles_m * tiles_n > INT32_MAX) {
+    set_last_error("w8a16_gemm: too many tiles");
+    return MI_ERR_INVALID;
+  }
+  GemmArgs a{static_cast<const unsigned char*>(x), reinterpret_cast<const unsigned char*>(w),
+             scales, y, x_sm, w_sn, s_sn, y_sm, (int32_t)m, (int32_t)n, (int32_t)k,
+             (int32_t)tiles_m, (int32_t)tiles_n,
+             ((uintptr_t)y % 8 == 0 && y_sm % 4 == 0) ? 1 : 0};
+  dim3 grid((unsigned)(tiles_m * tiles_n)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+#define MI_GEMM(T, ST) hipLaunchKernelGGL((w8a16_gemm_kernel<T, ST>), grid, block, kGmLdsBytes, st, a)
+  if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_BF16) MI_GEMM(bf16_t, bf16_t);
+  else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F32) MI_GEMM(bf16_t, float);
+  else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F16) MI_GEMM(bf16_t, f16_t);
+  else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_F16) MI_GEMM(f16_t, f16_t);
+  else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_F32) MI_GEMM(f16_t, float);
+  else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_BF16) MI_GEMM(f16_t, bf16_t);
+  else {
+    set_last_error("w8a16_gemm: activations must be bf16 or fp16 (dtype %d, scales %d)",
+                   (int)dtype, (int)sdtype);
+    return MI_ERR_UNSUPPORTED;
+  }
+#undef MI_GEMM
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_last_error("w8a16_gemm: launch failed: %s", hipGetErrorString(e));
+    return (int32_t)e;
+  }
+  return MI_OK;
+}

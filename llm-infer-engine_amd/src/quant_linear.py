@@ -3,8 +3,12 @@
 Int8 weights [N, K] with per-row scales [N, 1]; y = (x.f32 @ q.f32^T) * s in
 fp32, stored in x's dtype.  Decode-sized inputs (M <= 8 rows, the reference's
 threshold at src/quant_linear.py:273) run the MFMA GEMV kernel mi_w8a16_gemv,
-which reads every weight byte once for all rows.  Larger M is served by the
-same kernel in 16-row slices (correct, not tuned for prefill).
+which reads every weight byte once for all rows.  Prefill-sized inputs run the
+MFMA GEMM mi_w8a16_gemm (128 x 256 output tiles, int8 weight fragments widened
+in registers).  Between the two, and for K not a multiple of 64, the GEMV
+kernel serves the rows in 16-row slices: below GEMM_MIN_ROWS rows (three
+slices) the slices are faster than the GEMM, whose grid has a single row of
+tiles there.
 """
 from __future__ import annotations
 
@@ -14,6 +18,8 @@ import torch.nn as nn
 from . import _lib
 
 _GEMV_MAX_ROWS = 16
+GEMM_MIN_ROWS = 48      # rows from which w8a16_gemm_launch uses the GEMM kernel
+_GEMM_K_STEP = 64
 
 
 def _prep(x, weight, scales):
@@ -59,8 +65,33 @@ def w8a16_gemv_launch(x, weight, scales, *, block_n: int = 32, block_k: int = 25
     return out
 
 
+def gemm_supported(M: int, K: int) -> bool:
+    """Whether w8a16_gemm_launch runs the GEMM kernel for an [M, K] input."""
+    return M >= GEMM_MIN_ROWS and K % _GEMM_K_STEP == 0
+
+
+def w8a16_gemm_mfma(x, weight, scales):
+    """The GEMM kernel for any M (K % 64 == 0): x [M, K] -> [M, N]."""
+    x, w, s = _prep(x, weight, scales)
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    M, K = x.shape
+    N = w.shape[0]
+    out = torch.empty((M, N), device=x.device, dtype=x.dtype)
+    st = _lib.load().mi_w8a16_gemm(
+        x.data_ptr(), w.data_ptr(), s.data_ptr(), out.data_ptr(), M, N, K,
+        x.stride(0), w.stride(0), s.stride(0), out.stride(0),
+        _lib.dtype_code(x.dtype), _lib.dtype_code(s.dtype), _lib.stream_of(x))
+    _lib.check(st, "w8a16_gemm")
+    return out
+
+
 def w8a16_gemm_launch(x, weight, scales, *, block_m: int = 64, block_n: int = 64, block_k: int = 128):
-    """Same contract as w8a16_gemv_launch for any M (src/quant_linear.py:191-247)."""
+    """Same contract as w8a16_gemv_launch for any M (src/quant_linear.py:191-247).
+    block_m/block_n/block_k are accepted for signature compatibility (the
+    MFMA tiling is fixed)."""
+    if gemm_supported(x.shape[0], x.shape[1]):
+        return w8a16_gemm_mfma(x, weight, scales)
     return w8a16_gemv_launch(x, weight, scales)
 
 

@@ -124,3 +124,39 @@ def test_lm_head_python_rules_without_gpu():
         lh.lm_head(torch.zeros(4, 512, dtype=torch.float16), w)
     with pytest.raises(ValueError, match="CUDA"):
         lh.lm_head(torch.zeros(4, 512, dtype=torch.bfloat16), w)
+
+
+def _gemm_call(lib, **over):
+    a = dict(x=1 << 20, w=1 << 21, s=1 << 22, y=1 << 23, m=300, n=1000, k=2048,
+             x_sm=2048, w_sn=2048, s_sn=1, y_sm=1000, dtype=0, sdtype=0)
+    a.update(over)
+    return lib.mi_w8a16_gemm(a["x"], a["w"], a["s"], a["y"], a["m"], a["n"], a["k"],
+                             a["x_sm"], a["w_sn"], a["s_sn"], a["y_sm"], a["dtype"],
+                             a["sdtype"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    ({"w": None}, -1, "null"),
+    ({"m": 0}, -1, "positive"),
+    ({"k": 1000, "x_sm": 1000, "w_sn": 1008}, -2, "multiple of 64"),
+    ({"x_sm": 1024}, -1, "strides"),
+    ({"y_sm": 999}, -1, "strides"),
+    ({"w_sn": 1 << 24}, -1, "strides"),
+    ({"x": (1 << 20) + 8}, -1, "aligned"),
+    ({"x_sm": 2052}, -1, "aligned"),
+    ({"w_sn": 2056}, -1, "aligned"),
+    ({"dtype": 2, "sdtype": 2}, -2, "bf16 or fp16"),
+])
+def test_w8a16_gemm_c_side_validation(over, code, msg):
+    """mi_w8a16_gemm rejects bad calls before touching the device."""
+    from src import _lib
+    lib = _lib.load()
+    assert _gemm_call(lib, **over) == code
+    assert msg in _lib.last_error()
+
+
+def test_w8a16_gemm_dispatch_rule():
+    from src.quant_linear import gemm_supported, GEMM_MIN_ROWS
+    assert GEMM_MIN_ROWS > 8                       # M <= 8 is the GEMV side (src/quant_linear.py:273)
+    assert gemm_supported(GEMM_MIN_ROWS, 2048) and not gemm_supported(GEMM_MIN_ROWS - 1, 2048)
+    assert not gemm_supported(4096, 80)            # K % 64 != 0: GEMV slices

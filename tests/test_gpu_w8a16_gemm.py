@@ -1,0 +1,116 @@
+"""GPU parity of the W8A16 prefill GEMM (mi_w8a16_gemm) against the CPU oracle.
+
+Shapes: the reference unit test's multi-row cases (tests/quant_unit.py:82-90,
+33 and 65 rows), the Llama-3.2-1B projection shapes at prefill sizes, and
+ragged M / N that leave partial 128 x 256 tiles.  Bars:
+  * one-hot activation rows select single weight columns, so every output is
+    one exact product q * s rounded once: bit-exact against the CPU rounding
+    of the same fp32 product (pins row/column/k indexing, the LDS swizzles,
+    the k permutation, the int8 widening and the scale index exactly);
+  * random inputs: within 2e-2 of the output scale of the fp32 oracle
+    (oracle.quant.w8a16, the reference test's reference), and within 1e-2 of
+    the GEMV kernel's result on the same rows (two fp32 summation orders).
+"""
+import pytest
+import torch
+
+from helpers import max_abs
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+
+
+def _quantised(N, K, dtype, dev, seed):
+    from src.quant_utils import quantize_weight_symmetric_per_channel
+    g = torch.Generator("cpu").manual_seed(seed)
+    w = torch.randn(N, K, generator=g).to(dtype).to(dev)
+    return quantize_weight_symmetric_per_channel(w)
+
+
+def _x(M, K, dtype, dev, seed):
+    g = torch.Generator("cpu").manual_seed(seed)
+    return torch.randn(M, K, generator=g).to(dtype).to(dev)
+
+
+def _rel(a, b):
+    return max_abs(a, b) / (float(b.float().abs().max()) + 1e-6)
+
+
+@pytest.mark.parametrize("M,K,N", [(33, 2048, 2048), (65, 512, 1024), (9, 256, 256), (1, 256, 256),
+                                   (128, 512, 256), (300, 1024, 1000), (257, 640, 1003)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_matches_oracle_and_gemv(dev, M, K, N, dtype):
+    from src.quant_linear import w8a16_gemm_mfma, w8a16_gemv_launch
+    q, s = _quantised(N, K, dtype, dev, 1)
+    x = _x(M, K, dtype, dev, 2)
+    y = w8a16_gemm_mfma(x, q, s)
+    assert y.shape == (M, N) and y.dtype == dtype
+    ref = oq.w8a16(x, q, s)
+    assert _rel(y, ref) < 2e-2
+    assert _rel(y, w8a16_gemv_launch(x, q, s)) < 1e-2
+
+
+@pytest.mark.parametrize("M,K,N", [(2048, 2048, 2048), (512, 2048, 8192), (1024, 8192, 2048),
+                                   (640, 2048, 512), (2048, 2048, 8192), (2000, 512, 8000)])
+def test_gemm_llama_projection_shapes(dev, M, K, N):
+    from src.quant_linear import w8a16_gemm_mfma
+    q, s = _quantised(N, K, torch.bfloat16, dev, 3)
+    x = _x(M, K, torch.bfloat16, dev, 4)
+    y = w8a16_gemm_mfma(x, q, s)
+    assert _rel(y, oq.w8a16(x, q, s)) < 2e-2
+
+
+@pytest.mark.parametrize("dtype,sdtype", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                          (torch.float16, torch.float16), (torch.float16, torch.float32)])
+@pytest.mark.parametrize("M,K,N", [(300, 256, 1000), (130, 512, 259), (128, 64, 256), (1900, 192, 8101)])
+def test_one_hot_rows_bit_exact(dev, dtype, sdtype, M, K, N):
+    """Row m of x is v_m * e_{k_m} (v_m a power of two): y[m, n] =
+    round(v_m * q[n, k_m] * s[n]) with a single exact fp32 product."""
+    from src.quant_linear import w8a16_gemm_mfma
+    q, s = _quantised(N, K, dtype, dev, 5)
+    s = s.to(sdtype)
+    g = torch.Generator("cpu").manual_seed(6)
+    k_of = torch.randint(0, K, (M,), generator=g)
+    v = torch.pow(2.0, torch.randint(-3, 4, (M,), generator=g).float()) * \
+        (torch.randint(0, 2, (M,), generator=g).float() * 2 - 1)
+    x = torch.zeros(M, K)
+    x[torch.arange(M), k_of] = v
+    y = w8a16_gemm_mfma(x.to(dtype).to(dev), q, s)
+    qc, sc = q.cpu().float(), s.cpu().float().reshape(-1)
+    expect = ((qc[:, k_of].t() * v[:, None]) * sc[None, :]).to(dtype)
+    assert torch.equal(y.cpu(), expect)
+
+
+def test_strided_rows_and_output_padding(dev):
+    """x with a row stride wider than K; y written through the C ABI into a
+    wider buffer: columns past N keep their sentinel."""
+    from src import _lib
+    M, K, N = 200, 512, 1001
+    q, s = _quantised(N, K, torch.bfloat16, dev, 7)
+    base = _x(M, K + 64, torch.bfloat16, dev, 8)
+    x = base[:, :K]
+    y = torch.full((M, N + 7), 7.0, device=dev, dtype=torch.bfloat16)
+    st = _lib.load().mi_w8a16_gemm(
+        x.data_ptr(), q.data_ptr(), s.data_ptr(), y.data_ptr(), M, N, K,
+        x.stride(0), q.stride(0), s.stride(0), y.stride(0),
+        _lib.dtype_code(x.dtype), _lib.dtype_code(s.dtype), _lib.stream_of(x))
+    _lib.check(st, "w8a16_gemm")
+    assert _rel(y[:, :N], oq.w8a16(x, q, s)) < 2e-2
+    assert torch.all(y[:, N:] == 7.0)
+
+
+def test_linear_layer_dispatch(dev):
+    """W8A16Linear: M > 8 goes to w8a16_gemm_launch, which takes the GEMM
+    kernel from GEMM_MIN_ROWS rows (K % 64 == 0) and the GEMV slices below;
+    3-D input keeps its leading shape."""
+    from src.quant_linear import W8A16Linear, gemm_supported, GEMM_MIN_ROWS
+    K, N = 1024, 768
+    q, s = _quantised(N, K, torch.bfloat16, dev, 9)
+    layer = W8A16Linear(K, N).to(dev)
+    layer.weight.data, layer.scales.data = q, s
+    for M in (9, GEMM_MIN_ROWS - 1, GEMM_MIN_ROWS, 4 * 97):
+        x = _x(M, K, torch.bfloat16, dev, 10 + M)
+        y = layer(x.reshape(1, M, K))
+        assert y.shape == (1, M, N)
+        assert _rel(y.reshape(M, N), oq.w8a16(x, q, s)) < 2e-2
+    assert gemm_supported(GEMM_MIN_ROWS, K) and not gemm_supported(GEMM_MIN_ROWS, 80)
