@@ -295,6 +295,55 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
     return out
 
 
+def bench_loader(torch) -> dict:
+    """Checkpoint load of a Llama-3.2-1B-shaped Hugging Face safetensors file
+    (random bf16 values, tied embeddings, 2.47 GB) written to a temporary
+    directory: build_model_from_weights for bf16 and for W8A16 (on-device
+    quantisation).  The file was just written, so it is served from the page
+    cache: the figure is memcpy + host->HBM DMA + quantisation, not disk."""
+    import contextlib
+    import tempfile
+    from safetensors.torch import save_file
+    from src.config import ModelArgs
+    from src.loader import build_model_from_weights
+    from src.model import Llama3
+    dev = torch.device("cuda:0")
+    args = ModelArgs(max_seq_len=256, device=str(dev))
+    d, hd, kv = args.dim, args.hidden_dim, args.n_kv_heads * (args.dim // args.n_heads)
+    shapes = {"model.embed_tokens.weight": (args.vocab_size, d), "model.norm.weight": (d,)}
+    for i in range(args.n_layers):
+        p = f"model.layers.{i}."
+        shapes.update({p + "self_attn.q_proj.weight": (d, d), p + "self_attn.k_proj.weight": (kv, d),
+                       p + "self_attn.v_proj.weight": (kv, d), p + "self_attn.o_proj.weight": (d, d),
+                       p + "mlp.gate_proj.weight": (hd, d), p + "mlp.up_proj.weight": (hd, d),
+                       p + "mlp.down_proj.weight": (d, hd), p + "input_layernorm.weight": (d,),
+                       p + "post_attention_layernorm.weight": (d,)})
+    g = torch.Generator("cpu").manual_seed(0)
+    sd = {k: (torch.randn(s, generator=g) * 0.02).to(torch.bfloat16) for k, s in shapes.items()}
+    nbytes = sum(v.numel() * 2 for v in sd.values())
+    out = {"config": "Llama-3.2-1B-shaped HF safetensors, tied embeddings, random bf16, page-cached",
+           "bytes": nbytes, "unit": "GB/s"}
+    with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
+        path = os.path.join(tmp, "model.safetensors")
+        save_file(sd, path)
+        del sd
+        # the first load also pays one-time set-up (pinned staging buffers, the
+        # allocator's first HBM reservations, page-table population of the
+        # mapping): reported apart from the steady-state loads that follow
+        for label, quant in (("first_load_w8a16", "w8a16"), ("bf16", None), ("w8a16", "w8a16")):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            with contextlib.redirect_stdout(sys.stderr):   # the loader's progress lines
+                model, _ = build_model_from_weights(Llama3, args, path, str(dev),
+                                                    dtype=torch.bfloat16, quantization=quant)
+            torch.cuda.synchronize()
+            t = time.perf_counter() - t0
+            out[label] = {"seconds": round(t, 3), "GB_per_s": round(nbytes / t / 1e9, 2)}
+            del model
+    out["value"] = out["w8a16"]["GB_per_s"]
+    return out
+
+
 def cpu_baseline(torch) -> dict:
     """The fp32 CPU oracle on batch 0 of config 2 (1/4 of a step), on rank 0."""
     from oracle import attention as ora
@@ -328,7 +377,7 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one plain 1 GiB device copy (scales rocprofv3 FETCH/WRITE_SIZE)")
-    ap.add_argument("--only", choices=["prefill", "decode", "step", "gemm"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "step", "gemm", "load"], default=None,
                     help="run one leg only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -360,6 +409,8 @@ def main() -> None:
         extra["decode_step_config5"] = bench_config5(torch, args.steps, args.warmup)
     if args.only in (None, "gemm"):
         extra["w8a16_prefill_gemm"] = bench_w8a16_prefill(torch, args.steps, args.warmup)
+    if args.only == "load":    # host I/O; not part of the default run
+        extra["checkpoint_load"] = bench_loader(torch)
     cpu = None
     if not args.no_cpu_baseline and args.only is None:
         cpu = cpu_baseline(torch)
