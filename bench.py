@@ -289,7 +289,8 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
            "flops_per_step": flops, "per_projection": per,
            "roofline": {"bound": "mfma", "kernel": "w8a16_gemm_kernel (w1 shape)",
                         "achieved": dom["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(dom["tflops"] / BF16_PEAK_TFLOPS, 4), "traffic": None}}
+                        "frac": round(dom["tflops"] / BF16_PEAK_TFLOPS, 4),
+                        "traffic": _traffic("w8a16_gemm_traffic.md", "hbm_bytes_per_launch_w1")}}
     del xs, ws, ss, ys
     torch.cuda.empty_cache()
     return out
