@@ -228,6 +228,30 @@ int32_t mi_w8a16_gemm(const void* x, const int8_t* w, const void* scales,
                       int32_t sdtype, void* stream);
 
 /*
+ * Split count for mi_w8a16_gemm_splitk on the current device: 1 when the
+ * 128 x 256 output tiles alone occupy every CU (use mi_w8a16_gemm), else the
+ * number of K splits (each at least 128 deep, fp32 partials <= 64 MiB).
+ * Same interface role as mi_w8a16_gemm (src/quant_linear.py:191-247).
+ */
+int64_t mi_w8a16_gemm_splits(int64_t m, int64_t n, int64_t k);
+
+/*
+ * mi_w8a16_gemm for grids too small to occupy the GPU: the K range is split
+ * across `splits` workgroups per output tile, each writing unscaled fp32 sums
+ * to part[split][m][n] (caller's workspace, >= splits * m * n elements), then
+ * a second launch adds the splits in split order, applies scales[n] and
+ * rounds to x's dtype.  2 <= splits <= min(k / 64, 64); other requirements as
+ * mi_w8a16_gemm.  Replaces w8a16_gemm_kernel + w8a16_gemm_launch
+ *   src/quant_linear.py:123-188, src/quant_linear.py:191-247 (small M).
+ */
+int32_t mi_w8a16_gemm_splitk(const void* x, const int8_t* w, const void* scales,
+                             void* y, int64_t m, int64_t n, int64_t k,
+                             int64_t x_sm, int64_t w_sn, int64_t s_sn,
+                             int64_t y_sm, float* part, int64_t part_elems,
+                             int64_t splits, int32_t dtype, int32_t sdtype,
+                             void* stream);
+
+/*
  * Fused decode-step projection (1 <= m <= 16 rows; k one of 512, 1024, 1536,
  * 2048, 3072, 4096, 6144, 8192):
  *   a   = rmsnorm(x, norm_w, eps) if norm_w != NULL else x   (rounded to dtype)

@@ -29,6 +29,8 @@ constexpr float kNegBig = -1.0e30f;
 
 // ---------------------------------------------------------------- host side
 void set_last_error(const char* fmt, ...);
+// compute units of the current device (cached per device; 256 if unknown)
+int device_cu_count();
 
 // ---------------------------------------------------------- element traits
 template <typename T> struct Elem;

@@ -450,20 +450,6 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
 // ------------------------------------------------------------------ host
 namespace {
 
-int device_cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
-                              dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 int elem_bytes(int32_t dtype) { return dtype == MI_DTYPE_F32 ? 4 : 2; }
 
 int gc_max(int32_t dtype, int64_t D) {

@@ -281,12 +281,7 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(const float* part_v
 namespace {
 
 int lm_head_grid(int64_t n) {
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess) {
-    int c = 0;
-    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && c > 0)
-      cus = c;
-  }
+  const int cus = device_cu_count();
   const int64_t tiles = (n + 15) / 16;
   const int64_t groups = (tiles + kLmWaves - 1) / kLmWaves;
   return (int)(groups < 2 * cus ? groups : 2 * cus);

@@ -49,6 +49,11 @@ struct GemmArgs {
   int32_t M, N, K;
   int32_t tiles_m, tiles_n;
   int32_t y_vec;           // rows of y allow 8-byte stores of 4 columns
+  // split-K: workgroup (tile, split) sums stages [split * split_stages, +split_stages)
+  // into part[split][m][n] (fp32, rows of N); one split = the whole K
+  float* part;
+  int32_t split_stages;
+  int32_t part_vec;        // part rows allow 16-byte stores of 4 columns
 };
 
 constexpr int kGmBM = 128;                      // output rows (m) per workgroup
@@ -112,9 +117,8 @@ template <> struct GemmOps<f16_t> {
 // Tile of a linear workgroup id: ids dealt round-robin to the 8 XCDs are first
 // regrouped so that each XCD's ids are consecutive, then consecutive ids walk
 // groups of kGmGroupM m-tiles, m fastest.
-__device__ inline void gm_tile(const GemmArgs& a, int& tm, int& tn) {
+__device__ inline void gm_tile(const GemmArgs& a, int b, int& tm, int& tn) {
   const int G = a.tiles_m * a.tiles_n;
-  int b = blockIdx.x;
   if ((G & 7) == 0) b = (b & 7) * (G >> 3) + (b >> 3);
   const int group = kGmGroupM * a.tiles_n;
   const int g = b / group, first = g * kGmGroupM;
@@ -124,7 +128,7 @@ __device__ inline void gm_tile(const GemmArgs& a, int& tm, int& tn) {
   tn = in / gm;
 }
 
-template <typename T, typename ST>
+template <typename T, typename ST, bool PARTIAL>
 __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
   using OP = GemmOps<T>;
   typedef typename OP::v8 v8;
@@ -132,15 +136,19 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the wave's 64 columns
   const int r = lane & 31, h = lane >> 5;
+  // split-K: workgroup ids run over all tiles of split 0, then of split 1, ...
+  const int n_tiles = a.tiles_m * a.tiles_n;
+  const int split = PARTIAL ? (int)blockIdx.x / n_tiles : 0;
   int tm, tn;
-  gm_tile(a, tm, tn);
+  gm_tile(a, (int)blockIdx.x - split * n_tiles, tm, tn);
   const int m0 = tm * kGmBM, n0 = tn * kGmBN;
 
-  // the workgroup's 256 column scales as fp32 (read by the epilogue; published
-  // by the main loop's first barrier)
+  // the workgroup's 256 column scales as fp32, staged in LDS after the first
+  // stage's copies are issued (read by the epilogue; published by the main
+  // loop's first barrier)
+  const ST sc_raw =
+      reinterpret_cast<const ST*>(a.scales)[(int64_t)min(n0 + (int)threadIdx.x, a.N - 1) * a.s_sn];
   float* const sc_lds = reinterpret_cast<float*>(smem_raw + 2 * kGmXBytes);
-  sc_lds[threadIdx.x] = Elem<ST>::to_f32(
-      reinterpret_cast<const ST*>(a.scales)[(int64_t)min(n0 + (int)threadIdx.x, a.N - 1) * a.s_sn]);
 
   // ---- activation DMA: instruction i of wave wv copies tile rows
   // 8 (4 wv + i) .. + 8; lane t fetches logical chunk (t % 8) ^ swz(row) of
@@ -155,7 +163,8 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
   }
   const unsigned char* x_base = a.x + (int64_t)m0 * a.x_sm * 2;
   const uint32_t lds0 = lds_addr(smem_raw);
-  const int nk = a.K / kGmBK;
+  const int s_begin = PARTIAL ? split * a.split_stages : 0;
+  const int nk = PARTIAL ? min(s_begin + a.split_stages, a.K / kGmBK) : a.K / kGmBK;
   auto issue_x = [&](int s) {
     const uint32_t xl = lds0 + (s & 1) * kGmXBytes;
     const unsigned char* xb = x_base + (int64_t)s * kGmBK * 2;
@@ -232,9 +241,10 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
 
   // two register sets for the weight fragments, alternating by stage
   u32x4 wa[2][2], wb[2][2];
-  issue_x(0);
-  load_w(0, wa);
-  int s = 0;
+  issue_x(s_begin);
+  load_w(s_begin, wa);
+  sc_lds[threadIdx.x] = Elem<ST>::to_f32(sc_raw);
+  int s = s_begin;
   for (; s + 1 < nk; s += 2) {
     step(s, wa, wb);
     step(s + 1, wb, wa);
@@ -243,6 +253,31 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
 
   // ---- epilogue: acc[mf][nf][4 g + i] = C[n][m] with
   // n = n0 + 64 wv + 32 nf + 8 g + 4 h + i, m = m0 + 32 mf + r
+  if constexpr (PARTIAL) {
+    // unscaled fp32 sums of this split's k range
+    float* pp = a.part + (int64_t)split * a.M * a.N;
+#pragma unroll
+    for (int nf = 0; nf < 2; ++nf)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int nb = n0 + 64 * wv + 32 * nf + 8 * g + 4 * h;
+#pragma unroll
+        for (int mf = 0; mf < 4; ++mf) {
+          const int m = m0 + 32 * mf + r;
+          if (m >= a.M) continue;
+          float* q = pp + (int64_t)m * a.N + nb;
+          if (a.part_vec && nb + 3 < a.N) {
+            *reinterpret_cast<f32x4*>(q) = f32x4{acc[mf][nf][4 * g], acc[mf][nf][4 * g + 1],
+                                                 acc[mf][nf][4 * g + 2], acc[mf][nf][4 * g + 3]};
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (nb + i < a.N) q[i] = acc[mf][nf][4 * g + i];
+          }
+        }
+      }
+    return;
+  }
   T* y = reinterpret_cast<T*>(a.y);
 #pragma unroll
   for (int nf = 0; nf < 2; ++nf) {
@@ -271,64 +306,204 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
   }
 }
 
+// Split-K finish: y[m, n] = round((sum over splits, in split order, of
+// part[s][m][n]) * scale[n]); one thread per 4 consecutive columns of a row.
+template <typename T, typename ST>
+__global__ __launch_bounds__(256) void w8a16_splitk_reduce_kernel(GemmArgs a, int32_t splits) {
+  const int64_t q4 = (a.N + 3) / 4;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)a.M * q4) return;
+  const int m = (int)(idx / q4), nb = (int)(idx - (int64_t)m * q4) * 4;
+  const ST* sc = reinterpret_cast<const ST*>(a.scales);
+  const int64_t plane = (int64_t)a.M * a.N;
+  const float* pp = a.part + (int64_t)m * a.N + nb;
+  T* yp = reinterpret_cast<T*>(a.y) + (int64_t)m * a.y_sm + nb;
+  if (a.part_vec && nb + 3 < a.N) {
+    f32x4 t = *reinterpret_cast<const f32x4*>(pp);
+    for (int sp = 1; sp < splits; ++sp) t += *reinterpret_cast<const f32x4*>(pp + sp * plane);
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    t4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      v[i] = Elem<T>::from_f32(t[i] * Elem<ST>::to_f32(sc[(int64_t)(nb + i) * a.s_sn]));
+    if (a.y_vec) {
+      *reinterpret_cast<t4*>(yp) = v;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) yp[i] = v[i];
+    }
+  } else {
+    for (int i = 0; i < 4 && nb + i < a.N; ++i) {
+      float t = pp[i];
+      for (int sp = 1; sp < splits; ++sp) t += pp[i + sp * plane];
+      yp[i] = Elem<T>::from_f32(t * Elem<ST>::to_f32(sc[(int64_t)(nb + i) * a.s_sn]));
+    }
+  }
+}
+
 }  // namespace mi
 
 using namespace mi;
 
-extern "C" int32_t mi_w8a16_gemm(const void* x, const int8_t* w, const void* scales, void* y,
-                                 int64_t m, int64_t n, int64_t k, int64_t x_sm, int64_t w_sn,
-                                 int64_t s_sn, int64_t y_sm, int32_t dtype, int32_t sdtype,
-                                 void* stream) {
+namespace {
+
+// Argument checks shared by both entry points; fills `a` (no split).
+int32_t gemm_setup(const char* what, const void* x, const int8_t* w, const void* scales,
+                   void* y, int64_t m, int64_t n, int64_t k, int64_t x_sm, int64_t w_sn,
+                   int64_t s_sn, int64_t y_sm, GemmArgs& a) {
   if (x == nullptr || w == nullptr || scales == nullptr || y == nullptr) {
-    set_last_error("w8a16_gemm: null pointer");
+    set_last_error("%s: null pointer", what);
     return MI_ERR_INVALID;
   }
   if (m <= 0 || n <= 0 || k <= 0 || m > INT32_MAX || n > INT32_MAX || k > INT32_MAX) {
-    set_last_error("w8a16_gemm: need positive M, N, K below 2^31 (M=%lld N=%lld K=%lld)",
+    set_last_error("%s: need positive M, N, K below 2^31 (M=%lld N=%lld K=%lld)", what,
                    (long long)m, (long long)n, (long long)k);
     return MI_ERR_INVALID;
   }
   if (k % kGmBK != 0) {
-    set_last_error("w8a16_gemm: K must be a multiple of %d (K=%lld)", kGmBK, (long long)k);
+    set_last_error("%s: K must be a multiple of %d (K=%lld)", what, kGmBK, (long long)k);
     return MI_ERR_UNSUPPORTED;
   }
   // tile-relative DMA offsets are 32-bit: 128 activation rows of x_sm elements
   if (x_sm < k || w_sn < k || y_sm < n || x_sm > (1LL << 23) || w_sn > (1LL << 23)) {
-    set_last_error("w8a16_gemm: row strides must cover a row and be below 2^23 elements");
+    set_last_error("%s: row strides must cover a row and be below 2^23 elements", what);
     return MI_ERR_INVALID;
   }
   if ((uintptr_t)x % 16 != 0 || (x_sm * 2) % 16 != 0 || (uintptr_t)w % 16 != 0 || w_sn % 16 != 0) {
-    set_last_error("w8a16_gemm: x and weight rows must be 16-byte aligned");
+    set_last_error("%s: x and weight rows must be 16-byte aligned", what);
     return MI_ERR_INVALID;
   }
   const int64_t tiles_m = (m + kGmBM - 1) / kGmBM, tiles_n = (n + kGmBN - 1) / kGmBN;
-  if (tiles_m * tiles_n > INT32_MAX) {
-    set_last_error("w8a16_gemm: too many tiles");
+  if (tiles_m * tiles_n > INT32_MAX / 64) {
+    set_last_error("%s: too many tiles", what);
     return MI_ERR_INVALID;
   }
-  GemmArgs a{static_cast<const unsigned char*>(x), reinterpret_cast<const unsigned char*>(w),
-             scales, y, x_sm, w_sn, s_sn, y_sm, (int32_t)m, (int32_t)n, (int32_t)k,
-             (int32_t)tiles_m, (int32_t)tiles_n,
-             ((uintptr_t)y % 8 == 0 && y_sm % 4 == 0) ? 1 : 0};
-  dim3 grid((unsigned)(tiles_m * tiles_n)), block(256);
-  hipStream_t st = (hipStream_t)stream;
-#define MI_GEMM(T, ST) hipLaunchKernelGGL((w8a16_gemm_kernel<T, ST>), grid, block, kGmLdsBytes, st, a)
+  a = GemmArgs{static_cast<const unsigned char*>(x), reinterpret_cast<const unsigned char*>(w),
+               scales, y, x_sm, w_sn, s_sn, y_sm, (int32_t)m, (int32_t)n, (int32_t)k,
+               (int32_t)tiles_m, (int32_t)tiles_n,
+               ((uintptr_t)y % 8 == 0 && y_sm % 4 == 0) ? 1 : 0,
+               nullptr, (int32_t)(k / kGmBK), 0};
+  return MI_OK;
+}
+
+bool dtypes_ok(int32_t dtype, int32_t sdtype) {
+  return (dtype == MI_DTYPE_BF16 || dtype == MI_DTYPE_F16) &&
+         (sdtype == MI_DTYPE_BF16 || sdtype == MI_DTYPE_F16 || sdtype == MI_DTYPE_F32);
+}
+
+template <bool PARTIAL>
+void launch_gemm(const GemmArgs& a, int32_t splits, int32_t dtype, int32_t sdtype, hipStream_t st) {
+  dim3 grid((unsigned)((int64_t)a.tiles_m * a.tiles_n * splits)), block(256);
+#define MI_GEMM(T, ST) \
+  hipLaunchKernelGGL((w8a16_gemm_kernel<T, ST, PARTIAL>), grid, block, kGmLdsBytes, st, a)
   if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_BF16) MI_GEMM(bf16_t, bf16_t);
   else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F32) MI_GEMM(bf16_t, float);
   else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F16) MI_GEMM(bf16_t, f16_t);
   else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_F16) MI_GEMM(f16_t, f16_t);
   else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_F32) MI_GEMM(f16_t, float);
-  else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_BF16) MI_GEMM(f16_t, bf16_t);
-  else {
+  else MI_GEMM(f16_t, bf16_t);
+#undef MI_GEMM
+}
+
+void launch_reduce(const GemmArgs& a, int32_t splits, int32_t dtype, int32_t sdtype,
+                   hipStream_t st) {
+  const int64_t threads = (int64_t)a.M * ((a.N + 3) / 4);
+  dim3 grid((unsigned)((threads + 255) / 256)), block(256);
+#define MI_RED(T, ST) \
+  hipLaunchKernelGGL((w8a16_splitk_reduce_kernel<T, ST>), grid, block, 0, st, a, splits)
+  if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_BF16) MI_RED(bf16_t, bf16_t);
+  else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F32) MI_RED(bf16_t, float);
+  else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F16) MI_RED(bf16_t, f16_t);
+  else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_F16) MI_RED(f16_t, f16_t);
+  else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_F32) MI_RED(f16_t, float);
+  else MI_RED(f16_t, bf16_t);
+#undef MI_RED
+}
+
+int32_t launch_status(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_last_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return (int32_t)e;
+  }
+  return MI_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t mi_w8a16_gemm(const void* x, const int8_t* w, const void* scales, void* y,
+                                 int64_t m, int64_t n, int64_t k, int64_t x_sm, int64_t w_sn,
+                                 int64_t s_sn, int64_t y_sm, int32_t dtype, int32_t sdtype,
+                                 void* stream) {
+  GemmArgs a;
+  int32_t rc = gemm_setup("w8a16_gemm", x, w, scales, y, m, n, k, x_sm, w_sn, s_sn, y_sm, a);
+  if (rc != MI_OK) return rc;
+  if (!dtypes_ok(dtype, sdtype)) {
     set_last_error("w8a16_gemm: activations must be bf16 or fp16 (dtype %d, scales %d)",
                    (int)dtype, (int)sdtype);
     return MI_ERR_UNSUPPORTED;
   }
-#undef MI_GEMM
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    set_last_error("w8a16_gemm: launch failed: %s", hipGetErrorString(e));
-    return (int32_t)e;
+  launch_gemm<false>(a, 1, dtype, sdtype, (hipStream_t)stream);
+  return launch_status("w8a16_gemm");
+}
+
+// Split count for mi_w8a16_gemm_splitk (measured on MI355X): 1 (no split) once
+// the 128 x 256 tiles give half the CUs a workgroup (the partials' traffic and
+// the reduce launch then cost more than the longer per-workgroup chain);
+// otherwise about one workgroup per CU, each split at least 8 stages (512 k)
+// deep, at most 8 splits, and the fp32 partials (written and read once) at
+// most 64 MiB.
+extern "C" int64_t mi_w8a16_gemm_splits(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % kGmBK != 0) return 1;
+  const int64_t tiles = ((m + kGmBM - 1) / kGmBM) * ((n + kGmBN - 1) / kGmBN);
+  const int64_t cus = device_cu_count();
+  if (2 * tiles >= cus) return 1;
+  int64_t s = cus / tiles;
+  const int64_t nk = k / kGmBK;
+  if (s > nk / 8) s = nk / 8;
+  if (s > 8) s = 8;
+  while (s > 1 && s * m * n * 4 > (64LL << 20)) --s;
+  // splits actually used: every split gets ceil(nk / s) stages
+  if (s > 1) {
+    const int64_t per = (nk + s - 1) / s;
+    s = (nk + per - 1) / per;
   }
-  return MI_OK;
+  return s < 1 ? 1 : s;
+}
+
+extern "C" int32_t mi_w8a16_gemm_splitk(const void* x, const int8_t* w, const void* scales,
+                                        void* y, int64_t m, int64_t n, int64_t k,
+                                        int64_t x_sm, int64_t w_sn, int64_t s_sn, int64_t y_sm,
+                                        float* part, int64_t part_elems, int64_t splits,
+                                        int32_t dtype, int32_t sdtype, void* stream) {
+  GemmArgs a;
+  int32_t rc = gemm_setup("w8a16_gemm_splitk", x, w, scales, y, m, n, k, x_sm, w_sn, s_sn, y_sm, a);
+  if (rc != MI_OK) return rc;
+  if (!dtypes_ok(dtype, sdtype)) {
+    set_last_error("w8a16_gemm_splitk: activations must be bf16 or fp16 (dtype %d, scales %d)",
+                   (int)dtype, (int)sdtype);
+    return MI_ERR_UNSUPPORTED;
+  }
+  const int64_t nk = k / kGmBK;
+  if (splits < 2 || splits > nk || splits > 64) {
+    set_last_error("w8a16_gemm_splitk: need 2 <= splits <= min(K / %d, 64) (splits=%lld)", kGmBK,
+                   (long long)splits);
+    return MI_ERR_INVALID;
+  }
+  const int64_t per = (nk + splits - 1) / splits;
+  const int64_t used = (nk + per - 1) / per;   // splits that own at least one stage
+  if (part == nullptr || part_elems < used * m * n) {
+    set_last_error("w8a16_gemm_splitk: workspace needs %lld fp32 elements (given %lld)",
+                   (long long)(used * m * n), (long long)part_elems);
+    return MI_ERR_INVALID;
+  }
+  a.part = part;
+  a.split_stages = (int32_t)per;
+  a.part_vec = ((uintptr_t)part % 16 == 0 && n % 4 == 0) ? 1 : 0;
+  hipStream_t st = (hipStream_t)stream;
+  launch_gemm<true>(a, (int32_t)used, dtype, sdtype, st);
+  rc = launch_status("w8a16_gemm_splitk");
+  if (rc != MI_OK) return rc;
+  launch_reduce(a, (int32_t)used, dtype, sdtype, st);
+  return launch_status("w8a16_gemm_splitk");
 }

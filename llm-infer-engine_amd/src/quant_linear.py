@@ -5,10 +5,10 @@ fp32, stored in x's dtype.  Decode-sized inputs (M <= 8 rows, the reference's
 threshold at src/quant_linear.py:273) run the MFMA GEMV kernel mi_w8a16_gemv,
 which reads every weight byte once for all rows.  Prefill-sized inputs run the
 MFMA GEMM mi_w8a16_gemm (128 x 256 output tiles, int8 weight fragments widened
-in registers).  Between the two, and for K not a multiple of 64, the GEMV
-kernel serves the rows in 16-row slices: below GEMM_MIN_ROWS rows (three
-slices) the slices are faster than the GEMM, whose grid has a single row of
-tiles there.
+in registers), with K split across workgroups (mi_w8a16_gemm_splitk) when the
+tiles alone cannot occupy the GPU.  Between the two, and for K not a multiple
+of 64, the GEMV kernel serves the rows in 16-row slices: below GEMM_MIN_ROWS
+rows (two slices) the slices are faster.
 """
 from __future__ import annotations
 
@@ -18,7 +18,7 @@ import torch.nn as nn
 from . import _lib
 
 _GEMV_MAX_ROWS = 16
-GEMM_MIN_ROWS = 48      # rows from which w8a16_gemm_launch uses the GEMM kernel
+GEMM_MIN_ROWS = 33      # rows from which w8a16_gemm_launch uses the GEMM kernels
 _GEMM_K_STEP = 64
 
 
@@ -70,19 +70,31 @@ def gemm_supported(M: int, K: int) -> bool:
     return M >= GEMM_MIN_ROWS and K % _GEMM_K_STEP == 0
 
 
-def w8a16_gemm_mfma(x, weight, scales):
-    """The GEMM kernel for any M (K % 64 == 0): x [M, K] -> [M, N]."""
+def w8a16_gemm_mfma(x, weight, scales, *, splits: int | None = None):
+    """The GEMM kernels for any M (K % 64 == 0): x [M, K] -> [M, N].
+
+    Grids of 128 x 256 tiles that do not occupy the GPU split K across
+    workgroups (fp32 partials in a workspace, then one reduce launch); the
+    split count comes from mi_w8a16_gemm_splits unless `splits` is given
+    (1 = no split)."""
     x, w, s = _prep(x, weight, scales)
     if x.stride(1) != 1:
         x = x.contiguous()
     M, K = x.shape
     N = w.shape[0]
+    lib = _lib.load()
     out = torch.empty((M, N), device=x.device, dtype=x.dtype)
-    st = _lib.load().mi_w8a16_gemm(
-        x.data_ptr(), w.data_ptr(), s.data_ptr(), out.data_ptr(), M, N, K,
-        x.stride(0), w.stride(0), s.stride(0), out.stride(0),
-        _lib.dtype_code(x.dtype), _lib.dtype_code(s.dtype), _lib.stream_of(x))
-    _lib.check(st, "w8a16_gemm")
+    S = lib.mi_w8a16_gemm_splits(M, N, K) if splits is None else int(splits)
+    args = (x.data_ptr(), w.data_ptr(), s.data_ptr(), out.data_ptr(), M, N, K,
+            x.stride(0), w.stride(0), s.stride(0), out.stride(0))
+    codes = (_lib.dtype_code(x.dtype), _lib.dtype_code(s.dtype), _lib.stream_of(x))
+    if S > 1:
+        part = torch.empty(S * M * N, device=x.device, dtype=torch.float32)
+        st = lib.mi_w8a16_gemm_splitk(*args, part.data_ptr(), part.numel(), S, *codes)
+        _lib.check(st, "w8a16_gemm_splitk")
+    else:
+        st = lib.mi_w8a16_gemm(*args, *codes)
+        _lib.check(st, "w8a16_gemm")
     return out
 
 

@@ -160,3 +160,52 @@ def test_w8a16_gemm_dispatch_rule():
     assert GEMM_MIN_ROWS > 8                       # M <= 8 is the GEMV side (src/quant_linear.py:273)
     assert gemm_supported(GEMM_MIN_ROWS, 2048) and not gemm_supported(GEMM_MIN_ROWS - 1, 2048)
     assert not gemm_supported(4096, 80)            # K % 64 != 0: GEMV slices
+
+
+def _splitk_call(lib, **over):
+    a = dict(x=1 << 20, w=1 << 21, s=1 << 22, y=1 << 23, m=300, n=1000, k=2048,
+             x_sm=2048, w_sn=2048, s_sn=1, y_sm=1000, part=1 << 24, part_elems=8 * 300 * 1000,
+             splits=8, dtype=0, sdtype=0)
+    a.update(over)
+    return lib.mi_w8a16_gemm_splitk(a["x"], a["w"], a["s"], a["y"], a["m"], a["n"], a["k"],
+                                    a["x_sm"], a["w_sn"], a["s_sn"], a["y_sm"], a["part"],
+                                    a["part_elems"], a["splits"], a["dtype"], a["sdtype"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    ({"splits": 1}, -1, "splits"),
+    ({"splits": 33}, -1, "splits"),               # K / 64 = 32 stages
+    ({"part": None}, -1, "workspace"),
+    ({"part_elems": 8 * 300 * 1000 - 1}, -1, "workspace"),
+    ({"k": 1000, "x_sm": 1000, "w_sn": 1008}, -2, "multiple of 64"),
+    ({"x": None}, -1, "null"),
+    ({"dtype": 2}, -2, "bf16 or fp16"),
+])
+def test_w8a16_gemm_splitk_c_side_validation(over, code, msg):
+    from src import _lib
+    lib = _lib.load()
+    assert _splitk_call(lib, **over) == code
+    assert msg in _lib.last_error()
+
+
+def test_w8a16_gemm_split_rule():
+    """Splits only for grids under one 128 x 256 tile per two CUs (256 CUs
+    without a device): about one workgroup per CU, each split >= 8 stages,
+    <= 8 splits, partials <= 64 MiB, and a count every split owns stages of."""
+    from src import _lib
+    lib = _lib.load()
+    assert lib.mi_w8a16_gemm_splits(8192, 2048, 2048) == 1        # 512 tiles
+    assert lib.mi_w8a16_gemm_splits(2048, 2048, 2048) == 1        # 128 tiles: half the CUs
+    assert lib.mi_w8a16_gemm_splits(128, 2048, 2048) == 4         # 8 tiles, 32 stages
+    assert lib.mi_w8a16_gemm_splits(512, 2048, 8192) == 8         # 32 tiles, 128 stages (K = 8192)
+    assert lib.mi_w8a16_gemm_splits(128, 2048, 1024) == 2         # 16 stages -> 8 deep each
+    assert lib.mi_w8a16_gemm_splits(128, 2048, 512) == 1          # 8 stages: too shallow
+    assert lib.mi_w8a16_gemm_splits(100, 1000, 1000) == 1         # K % 64 != 0
+    for m, n, k in [(48, 2048, 2048), (512, 2048, 2048), (700, 512, 8192), (256, 8192, 2048),
+                    (130, 3000, 1984), (2048, 2048, 512)]:
+        s = lib.mi_w8a16_gemm_splits(m, n, k)
+        nk = k // 64
+        assert 1 <= s <= 8 and (s == 1 or s * m * n * 4 <= 64 << 20)
+        if s > 1:
+            per = -(-nk // s)
+            assert -(-nk // per) == s and per >= 8

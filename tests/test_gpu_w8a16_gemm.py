@@ -114,3 +114,59 @@ def test_linear_layer_dispatch(dev):
         assert y.shape == (1, M, N)
         assert _rel(y.reshape(M, N), oq.w8a16(x, q, s)) < 2e-2
     assert gemm_supported(GEMM_MIN_ROWS, K) and not gemm_supported(GEMM_MIN_ROWS, 80)
+
+
+@pytest.mark.parametrize("splits", [2, 3, 7, 16])
+@pytest.mark.parametrize("M,K,N,dtype", [(33, 2048, 2048, torch.bfloat16), (65, 512, 1024, torch.float16),
+                                         (300, 1024, 1000, torch.bfloat16),
+                                         (257, 1152, 1003, torch.bfloat16)])
+def test_split_k_matches_oracle_and_unsplit(dev, M, K, N, dtype, splits):
+    """Split-K (fp32 partials + ordered reduce) against the oracle and the
+    single-pass kernel; 7 splits of 16/18 stages leave uneven split depths."""
+    from src.quant_linear import w8a16_gemm_mfma
+    if splits > K // 64:
+        pytest.skip("more splits than 64-deep stages")
+    q, s = _quantised(N, K, dtype, dev, 11)
+    x = _x(M, K, dtype, dev, 12)
+    y = w8a16_gemm_mfma(x, q, s, splits=splits)
+    assert y.shape == (M, N) and y.dtype == dtype
+    assert _rel(y, oq.w8a16(x, q, s)) < 2e-2
+    assert _rel(y, w8a16_gemm_mfma(x, q, s, splits=1)) < 1e-2
+
+
+@pytest.mark.parametrize("splits", [4, 16])
+def test_split_k_one_hot_rows_bit_exact(dev, splits):
+    """With one nonzero product per output the split sums are exact, so the
+    split path is bit-exact like the single pass."""
+    from src.quant_linear import w8a16_gemm_mfma
+    M, K, N = 130, 1024, 259
+    q, s = _quantised(N, K, torch.bfloat16, dev, 13)
+    g = torch.Generator("cpu").manual_seed(14)
+    k_of = torch.randint(0, K, (M,), generator=g)
+    x = torch.zeros(M, K)
+    x[torch.arange(M), k_of] = 1.0
+    y = w8a16_gemm_mfma(x.to(torch.bfloat16).to(dev), q, s, splits=splits)
+    expect = (q.cpu().float()[:, k_of].t() * s.cpu().float().reshape(-1)[None, :]).to(torch.bfloat16)
+    assert torch.equal(y.cpu(), expect)
+
+
+def test_split_k_default_rule_and_strided_output(dev):
+    """The library's split count is used by default for small grids; the
+    reduce honours a wider output row stride (columns past N untouched)."""
+    from src import _lib
+    from src.quant_linear import w8a16_gemm_mfma
+    M, K, N = 96, 2048, 1536
+    lib = _lib.load()
+    S = lib.mi_w8a16_gemm_splits(M, N, K)
+    assert S > 1
+    q, s = _quantised(N, K, torch.bfloat16, dev, 15)
+    x = _x(M, K, torch.bfloat16, dev, 16)
+    assert _rel(w8a16_gemm_mfma(x, q, s), oq.w8a16(x, q, s)) < 2e-2
+    y = torch.full((M, N + 5), 3.0, device=dev, dtype=torch.bfloat16)
+    part = torch.empty(S * M * N, device=dev, dtype=torch.float32)
+    st = lib.mi_w8a16_gemm_splitk(x.data_ptr(), q.data_ptr(), s.data_ptr(), y.data_ptr(), M, N, K,
+                                  x.stride(0), q.stride(0), s.stride(0), y.stride(0),
+                                  part.data_ptr(), part.numel(), S, 0, 0, _lib.stream_of(x))
+    _lib.check(st, "w8a16_gemm_splitk")
+    assert _rel(y[:, :N], oq.w8a16(x, q, s)) < 2e-2
+    assert torch.all(y[:, N:] == 3.0)
