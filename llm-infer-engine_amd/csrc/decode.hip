@@ -371,7 +371,8 @@ struct CombineArgs {
 // l_s > 0 (src/flash_decode.py:182-192), numerator over splits in float4
 // columns, out = num/den or 0/NaN for empty rows (src/flash_decode.py:203-205).
 // Latency-bound (a few KB per row): every thread issues all of its partial
-// loads before it reduces, so a call costs ~2 L2 round trips, not one per split.
+// loads (m, l and its first 8 numerator rows) before it reduces, so a call of
+// up to 256 splits costs one round trip to the partials, not one per split.
 template <typename T>
 __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
   constexpr int kUnroll = 8;
@@ -387,9 +388,27 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
   float* sacc = smem + S;  // [NSP][D] partial numerators
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
 
+  // Every load of the first pass is issued before any reduction: this
+  // thread's (m, l) of split `tid` and its numerator columns of splits
+  // sp, sp + nsp, ... (the barriers below would otherwise order the numerator
+  // loads behind the max and the denominator: two round trips instead of one).
+  const int ncol = D >> 2;
+  const int nsp = 256 / ncol;
+  const int c = tid % ncol, sp = tid / ncol;
+  const bool own = tid < S;                       // splits past 256: loops below
+  const float my_m = own ? pm[tid] : kNegBig;
+  const float my_l = own ? pl[tid] : 0.f;
+  f32x4 pv[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int s = sp + u * nsp;
+    pv[u] = s < S ? *reinterpret_cast<const f32x4*>(pacc + (int64_t)s * D + 4 * c)
+                  : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
   // max over non-empty splits
-  float mx = kNegBig;
-  for (int s = tid; s < S; s += 256)
+  float mx = my_l > 0.f ? my_m : kNegBig;
+  for (int s = tid + 256; s < S; s += 256)
     if (pl[s] > 0.f) mx = fmaxf(mx, pm[s]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, shfl_xor_f32(mx, off));
@@ -398,7 +417,12 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
   const float M = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
 
   float den = 0.f;
-  for (int s = tid; s < S; s += 256) {
+  if (own) {
+    const float wt = my_l > 0.f ? fast_exp2(my_m - M) : 0.f;
+    sw[tid] = wt;
+    den = wt * my_l;
+  }
+  for (int s = tid + 256; s < S; s += 256) {
     const float ls = pl[s];
     const float wt = ls > 0.f ? fast_exp2(pm[s] - M) : 0.f;
     sw[s] = wt;
@@ -410,12 +434,14 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
   __syncthreads();  // also publishes sw[]
   den = red[1][0] + red[1][1] + red[1][2] + red[1][3];
 
-  const int ncol = D >> 2;
-  const int nsp = 256 / ncol;
-  const int c = tid % ncol, sp = tid / ncol;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  for (int s0 = sp; s0 < S; s0 += nsp * kUnroll) {
-    f32x4 pv[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int s = sp + u * nsp;
+    const float wt = s < S ? sw[s] : 0.f;
+    if (wt != 0.f) acc += wt * pv[u];
+  }
+  for (int s0 = sp + nsp * kUnroll; s0 < S; s0 += nsp * kUnroll) {
     float wt[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
