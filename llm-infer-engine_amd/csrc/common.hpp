@@ -131,6 +131,23 @@ __device__ inline u32x4 load16_stream(const void* p) {
   return __builtin_nontemporal_load(q);
 }
 
+// Raw buffer resource over [base, base + bytes).  A 16-byte load at a byte
+// offset past `bytes` returns zeros and touches no memory (the hardware range
+// check): padding lanes of a tile pass kOobOffset and read nothing.
+typedef __amdgpu_buffer_rsrc_t buf_rsrc;
+constexpr uint32_t kOobOffset = 0x7ffffff0u;
+__device__ inline buf_rsrc make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ inline u32x4 buf_load16(buf_rsrc r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+// non-temporal variant (read-once weight streams)
+__device__ inline u32x4 buf_load16_nt(buf_rsrc r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2));
+}
+
 // ------------------------------------------------- LDS tile staging
 // One wave-wide 16-byte-per-lane global->LDS copy: lane t's 16 bytes at
 // base + voff land at LDS byte address lds + 16 t.  Issued as inline asm on

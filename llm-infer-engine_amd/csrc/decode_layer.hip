@@ -168,21 +168,30 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
   const int n_in_mat = tile_row<EPI, RPB>(tile, r, a.D);   // this lane's weight row
   const int n_valid = EPI == kEpiQkvRope ? (mat == 0 ? a.Hq : a.Hkv) * a.D : a.N;
   const bool row_ok = r < RPB && n_in_mat < n_valid;
-  const int8_t* wrow0 = wm + (int64_t)(row_ok ? n_in_mat : 0) * w_sn;
-  const int8_t* wrow1 = NMAT == 2 ? a.w1 + (int64_t)(row_ok ? n_in_mat : 0) * a.w_sn1 : nullptr;
+  // weight rows through buffer resources (host-checked: the matrix spans < 2^31 bytes):
+  // lanes of padding rows (r >= RPB, n >= N) get an out-of-range offset and
+  // load zeros without a memory access
+  const buf_rsrc wr0 = make_rsrc(wm, (uint32_t)((int64_t)(n_valid - 1) * w_sn + a.K));
+  const uint32_t wo0 = row_ok ? (uint32_t)((int64_t)n_in_mat * w_sn) : kOobOffset;
+  const buf_rsrc wr1 = make_rsrc(NMAT == 2 ? a.w1 : wm,
+                                 NMAT == 2 ? (uint32_t)((int64_t)(a.N - 1) * a.w_sn1 + a.K) : 0u);
+  const uint32_t wo1 = NMAT == 2 && row_ok ? (uint32_t)((int64_t)n_in_mat * a.w_sn1) : kOobOffset;
 
   // ---- without the prologue the B operands come straight from global memory:
   //      request them all first (L2 hits, they retire ahead of the weights)
   const int c_lo = w * MAXC;
   const int mc = min(m, a.M - 1);             // columns m >= M are discarded
-  const T* xg = reinterpret_cast<const T*>(a.x) + (int64_t)mc * a.x_sm;
   u32x4 xr[NORM ? 1 : MAXC][2];
   if constexpr (!NORM) {
+    // x through a buffer resource (host-checked: ((M-1)*x_sm + K)*2 < 2^31):
+    // the B-operand columns m >= M load zeros without a memory access
+    const buf_rsrc xrs = make_rsrc(a.x, (uint32_t)(((int64_t)(a.M - 1) * a.x_sm + a.K) * sizeof(T)));
+    const uint32_t xo = m_ok ? (uint32_t)((int64_t)m * a.x_sm * sizeof(T)) : kOobOffset;
 #pragma unroll
     for (int i = 0; i < MAXC; ++i) {
       const int k0 = (c_lo + i) * 64 + 16 * g;
-      xr[i][0] = load16(xg + k0);
-      xr[i][1] = load16(xg + k0 + 8);
+      xr[i][0] = buf_load16(xrs, xo + (uint32_t)(k0 * sizeof(T)));
+      xr[i][1] = buf_load16(xrs, xo + (uint32_t)((k0 + 8) * sizeof(T)));
     }
   }
 
@@ -191,8 +200,8 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
 #pragma unroll
   for (int i = 0; i < MAXC; ++i) {
     const int k0 = (c_lo + i) * 64 + 16 * g;
-    wq[0][i] = load16_stream(wrow0 + k0);
-    if constexpr (NMAT == 2) wq[1][i] = load16_stream(wrow1 + k0);
+    wq[0][i] = buf_load16_nt(wr0, wo0 + (uint32_t)k0);
+    if constexpr (NMAT == 2) wq[1][i] = buf_load16_nt(wr1, wo1 + (uint32_t)k0);
   }
   // ---- epilogue operands (row scales, residual, RoPE table entries), issued
   //      behind the weights so the epilogue does not start with a round trip;
@@ -455,6 +464,11 @@ int32_t check_x(const void* x, int64_t M, int64_t K, int64_t x_sm, const void* n
     set_last_error("%s: x rows must be 16-byte aligned", what);
     return MI_ERR_INVALID;
   }
+  if (x_sm < 0 || ((M - 1) * x_sm + K) * 2 >= ((int64_t)1 << 31)) {
+    set_last_error("%s: x row stride %lld out of range (x must span < 2 GB)", what,
+                   (long long)x_sm);
+    return MI_ERR_UNSUPPORTED;
+  }
   if (norm_w != nullptr && ((uintptr_t)norm_w % 16 != 0 || M * K * 2 > 64 * 1024 ||
                             (M > 8 && K > 2048))) {
     set_last_error("%s: RMSNorm prologue needs a 16-byte aligned weight, M*K*2 <= 64 KB and "
@@ -464,13 +478,20 @@ int32_t check_x(const void* x, int64_t M, int64_t K, int64_t x_sm, const void* n
   return MI_OK;
 }
 
-int32_t check_w(const int8_t* w, const void* s, int64_t w_sn, const char* what) {
+int32_t check_w(const int8_t* w, const void* s, int64_t w_sn, int64_t rows, int64_t K,
+                const char* what) {
   if (w == nullptr || s == nullptr) {
     set_last_error("%s: null weight or scales", what);
     return MI_ERR_INVALID;
   }
   if ((uintptr_t)w % 16 != 0 || w_sn % 16 != 0) {
     set_last_error("%s: weight rows must be 16-byte aligned", what);
+    return MI_ERR_UNSUPPORTED;
+  }
+  // weight loads use 32-bit byte offsets into the matrix
+  if (w_sn < 0 || (rows - 1) * w_sn + K >= ((int64_t)1 << 31)) {
+    set_last_error("%s: weight matrix out of range (%lld rows x %lld-byte stride must span "
+                   "< 2 GB)", what, (long long)rows, (long long)w_sn);
     return MI_ERR_UNSUPPORTED;
   }
   return MI_OK;
@@ -489,7 +510,7 @@ extern "C" int32_t mi_w8a16_linear_fused(
   const char* what = "w8a16_linear_fused";
   int32_t st = check_x(x, M, K, x_sm, norm_w, dtype, what);
   if (st != MI_OK) return st;
-  if ((st = check_w(w_a, s_a, w_sn_a, what)) != MI_OK) return st;
+  if ((st = check_w(w_a, s_a, w_sn_a, N, K, what)) != MI_OK) return st;
   if (y == nullptr || N < 1 || N > INT32_MAX - 16) {
     set_last_error("%s: null output or bad N (%lld)", what, (long long)N);
     return MI_ERR_INVALID;
@@ -498,7 +519,7 @@ extern "C" int32_t mi_w8a16_linear_fused(
     set_last_error("%s: residual epilogue needs res", what);
     return MI_ERR_INVALID;
   }
-  if (epilogue == kEpiSwiglu && (st = check_w(w_b, s_b, w_sn_b, what)) != MI_OK) return st;
+  if (epilogue == kEpiSwiglu && (st = check_w(w_b, s_b, w_sn_b, N, K, what)) != MI_OK) return st;
   if (epilogue == kEpiSwiglu && K > 4096) {
     set_last_error("%s: the SwiGLU epilogue supports K <= 4096 (K=%lld)", what,
                    (long long)K);
@@ -543,9 +564,9 @@ extern "C" int32_t mi_w8a16_qkv_rope_append(
   const char* what = "w8a16_qkv_rope_append";
   int32_t st = check_x(x, M, K, x_sm, norm_w, dtype, what);
   if (st != MI_OK) return st;
-  if ((st = check_w(wq, sq, wq_sn, what)) != MI_OK) return st;
-  if ((st = check_w(wk, sk, wk_sn, what)) != MI_OK) return st;
-  if ((st = check_w(wv, sv, wv_sn, what)) != MI_OK) return st;
+  if ((st = check_w(wq, sq, wq_sn, n_heads * head_dim, K, what)) != MI_OK) return st;
+  if ((st = check_w(wk, sk, wk_sn, n_kv_heads * head_dim, K, what)) != MI_OK) return st;
+  if ((st = check_w(wv, sv, wv_sn, n_kv_heads * head_dim, K, what)) != MI_OK) return st;
   if (cos == nullptr || sin == nullptr || pos == nullptr || q_out == nullptr ||
       cache_k == nullptr || cache_v == nullptr || rope_rows < 1 || c_ss < head_dim / 2) {
     set_last_error("%s: null rope table, position, output or cache pointer", what);

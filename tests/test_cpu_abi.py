@@ -209,3 +209,37 @@ def test_w8a16_gemm_split_rule():
         if s > 1:
             per = -(-nk // s)
             assert -(-nk // per) == s and per >= 8
+
+
+def _fused_call(lib, **over):
+    a = dict(x=1 << 20, x_sm=2048, norm_w=None, w_a=1 << 21, s_a=1 << 22, w_sn_a=2048,
+             w_b=None, s_b=None, w_sn_b=0, res=None, res_sm=0, y=1 << 23, y_sm=2048,
+             M=8, N=2048, K=2048, epi=0, dtype=0)
+    a.update(over)
+    return lib.mi_w8a16_linear_fused(a["x"], a["x_sm"], a["norm_w"], 1e-5, a["w_a"], a["s_a"],
+                                     a["w_sn_a"], a["w_b"], a["s_b"], a["w_sn_b"], a["res"],
+                                     a["res_sm"], a["y"], a["y_sm"], a["M"], a["N"], a["K"],
+                                     a["epi"], a["dtype"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    ({"x": None}, -1, "null x"),
+    ({"M": 17}, -2, "1 <= M <= 16"),
+    ({"K": 2000}, -2, "1 <= M <= 16"),
+    ({"x_sm": 2052}, -1, "16-byte aligned"),
+    ({"x_sm": 1 << 28}, -2, "x row stride"),              # x spans >= 2 GB
+    ({"w_sn_a": 2056}, -2, "16-byte aligned"),
+    ({"N": 1 << 20}, -2, "weight matrix out of range"),   # 2^20 rows x 2 KB = 2 GB
+    ({"w_sn_a": 1 << 21}, -2, "weight matrix out of range"),
+    ({"epi": 1}, -1, "needs res"),
+    ({"epi": 2, "w_b": 1 << 24, "s_b": 1 << 25, "w_sn_b": 2048, "N": 1 << 20}, -2,
+     "weight matrix out of range"),
+    ({"epi": 7}, -1, "unknown epilogue"),
+])
+def test_w8a16_linear_fused_c_side_validation(over, code, msg):
+    """mi_w8a16_linear_fused rejects bad calls (including weight matrices and x
+    spans past the 32-bit buffer offsets its loads use) before touching the device."""
+    from src import _lib
+    lib = _lib.load()
+    assert _fused_call(lib, **over) == code
+    assert msg in _lib.last_error()
