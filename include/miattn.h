@@ -262,7 +262,8 @@ int32_t mi_w8a16_gemm_splitk(const void* x, const int8_t* w, const void* scales,
  *   2  y = dtype(dtype(silu(y_a)) * y_b), y_b from w_b / s_b  (SwiGLU, k <= 4096)
  * Weights int8 [n, k] with 16-byte aligned rows (row strides w_sn_* bytes),
  * scales in the activation dtype (bf16/fp16), x/res/y rows in elements.  With
- * norm_w, m*k*2 <= 64 KB and k <= 2048 above 8 rows.  Unsupported shapes
+ * norm_w, m*k*2 <= 64 KB and k <= 2048 above 8 rows.  Each weight matrix and
+ * x must span < 2 GB (32-bit buffer offsets).  Unsupported shapes
  * return MI_ERR_UNSUPPORTED.  Each step rounds where the reference's separate ops
  * round, so results equal the unfused chain up to fp32 summation order.
  * Replaces, fused into one launch: rmsnorm_triton  src/rms_norm.py:42-77;
