@@ -2,13 +2,16 @@
 
 Int8 weights [N, K] with per-row scales [N, 1]; y = (x.f32 @ q.f32^T) * s in
 fp32, stored in x's dtype.  Decode-sized inputs (M <= 8 rows, the reference's
-threshold at src/quant_linear.py:273) run the MFMA GEMV kernel mi_w8a16_gemv,
-which reads every weight byte once for all rows.  Prefill-sized inputs run the
+threshold at src/quant_linear.py:273) read every weight byte once for all
+rows: through the decode-step projection kernel (mi_w8a16_linear_fused with
+the plain store epilogue, every weight load issued before the first MFMA)
+when the shape is one it serves, otherwise through the MFMA GEMV kernel
+mi_w8a16_gemv (any K, strided x, fp32 scales).  Prefill-sized inputs run the
 MFMA GEMM mi_w8a16_gemm (128 x 256 output tiles, int8 weight fragments widened
 in registers), with K split across workgroups (mi_w8a16_gemm_splitk) when the
 tiles alone cannot occupy the GPU.  Between the two, and for K not a multiple
-of 64, the GEMV kernel serves the rows in 16-row slices: below GEMM_MIN_ROWS
-rows (two slices) the slices are faster.
+of 64, the small-M kernels serve the rows in 16-row slices: below
+GEMM_MIN_ROWS rows (two slices) the slices are faster.
 """
 from __future__ import annotations
 
@@ -51,6 +54,46 @@ def _gemv_rows(x, w, s, out):
         x.stride(0), x.stride(1), w.stride(0), s.stride(0), out.stride(0), out.stride(1),
         _lib.dtype_code(x.dtype), _lib.dtype_code(s.dtype), _lib.stream_of(x))
     _lib.check(st, "w8a16_gemv")
+
+
+# K values and row count the decode-step projection kernel serves
+_FUSED_K = (512, 1024, 1536, 2048, 3072, 4096, 6144, 8192)
+_FUSED_MAX_ROWS = 16
+
+
+def _fused_gemv_ok(x, w, s) -> bool:
+    M, K = x.shape
+    return (1 <= M <= _FUSED_MAX_ROWS and K in _FUSED_K
+            and x.dtype in (torch.bfloat16, torch.float16) and s.dtype == x.dtype
+            and s.stride(0) == 1 and w.stride(1) == 1 and w.data_ptr() % 16 == 0
+            and w.stride(0) % 16 == 0 and x.stride(1) == 1 and x.data_ptr() % 16 == 0
+            and (x.stride(0) * x.element_size()) % 16 == 0
+            and ((M - 1) * x.stride(0) + K) * 2 < (1 << 31)
+            and (w.shape[0] - 1) * w.stride(0) + K < (1 << 31))
+
+
+def _fused_rows(x, w, s, out):
+    M, K = x.shape
+    N = w.shape[0]
+    st = _lib.load().mi_w8a16_linear_fused(
+        x.data_ptr(), x.stride(0), None, 0.0, w.data_ptr(), s.data_ptr(), w.stride(0),
+        None, None, 0, None, 0, out.data_ptr(), out.stride(0), M, N, K,
+        0, _lib.dtype_code(x.dtype), _lib.stream_of(x))
+    _lib.check(st, "w8a16_linear_fused")
+
+
+def w8a16_rows(x, weight, scales):
+    """Small-M product (decode batches, and the rows below GEMM_MIN_ROWS): the
+    decode-step projection kernel in 16-row slices where it serves the shape,
+    else the GEMV kernel (same slices)."""
+    xp, w, s = _prep(x, weight, scales)
+    M = xp.shape[0]
+    if not _fused_gemv_ok(xp[:_FUSED_MAX_ROWS], w, s):
+        return w8a16_gemv_launch(x, weight, scales)
+    out = torch.empty((M, w.shape[0]), device=xp.device, dtype=xp.dtype)
+    for m0 in range(0, M, _FUSED_MAX_ROWS):
+        _fused_rows(xp[m0:m0 + _FUSED_MAX_ROWS], w, s, out[m0:m0 + _FUSED_MAX_ROWS])
+    return out
 
 
 def w8a16_gemv_launch(x, weight, scales, *, block_n: int = 32, block_k: int = 256):
@@ -104,7 +147,7 @@ def w8a16_gemm_launch(x, weight, scales, *, block_m: int = 64, block_n: int = 64
     MFMA tiling is fixed)."""
     if gemm_supported(x.shape[0], x.shape[1]):
         return w8a16_gemm_mfma(x, weight, scales)
-    return w8a16_gemv_launch(x, weight, scales)
+    return w8a16_rows(x, weight, scales)
 
 
 class W8A16Linear(nn.Module):
@@ -125,7 +168,7 @@ class W8A16Linear(nn.Module):
         orig_shape = x.shape
         x_2d = x.reshape(-1, self.in_features)
         if x_2d.shape[0] <= 8:
-            out_2d = w8a16_gemv_launch(x_2d, self.weight, self.scales, block_n=32, block_k=256)
+            out_2d = w8a16_rows(x_2d, self.weight, self.scales)
         else:
             out_2d = w8a16_gemm_launch(x_2d, self.weight, self.scales, block_m=64, block_n=64,
                                        block_k=128)

@@ -65,3 +65,21 @@ def test_model_args_defaults_are_llama_3_2_1b():
     assert (a.dim, a.n_layers, a.n_heads, a.n_kv_heads, a.vocab_size, a.hidden_dim) == \
         (2048, 16, 32, 8, 128256, 8192)
     assert (a.norm_eps, a.max_batch_size, a.max_seq_len, a.rope_theta) == (1e-5, 1, 4096, 500000.0)
+
+
+def test_small_m_w8a16_routing_rule():
+    """Which small-M products W8A16Linear sends to the decode-step projection
+    kernel (the rest run the GEMV kernel): bf16/fp16 x with unit k stride and
+    16-byte rows, scales in x's dtype, K in the kernel's set, <= 16 rows."""
+    import torch
+    from src.quant_linear import _fused_gemv_ok
+    x = torch.zeros(8, 2048, dtype=torch.bfloat16)
+    w = torch.zeros(2048, 2048, dtype=torch.int8)
+    s = torch.zeros(2048, dtype=torch.bfloat16)
+    assert _fused_gemv_ok(x, w, s)
+    assert _fused_gemv_ok(x.half(), w, s.half())
+    assert not _fused_gemv_ok(x, w, s.float())                           # fp32 scales
+    assert not _fused_gemv_ok(x[:, :2000], w[:, :2000], s)                # K not served
+    assert not _fused_gemv_ok(torch.zeros(17, 2048, dtype=torch.bfloat16), w, s)
+    assert not _fused_gemv_ok(x.float(), w, s.float())                    # fp32 x
+    assert not _fused_gemv_ok(torch.zeros(2048, 8, dtype=torch.bfloat16).t(), w, s)  # k stride

@@ -104,3 +104,20 @@ def test_rmsnorm(dev, dtype):
     tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
     assert y.dtype == dtype and y.shape == x.shape
     assert max_abs(y, ref) < tol * float(ref.float().abs().max())
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 2048, 2048), (1, 8192, 2048), (8, 2048, 2048),
+                                   (16, 1024, 512), (24, 2048, 1024), (3, 80, 100)])
+def test_w8a16_gemv_kernel_and_small_m_route(dev, M, K, N):
+    """The GEMV kernel (mi_w8a16_gemv) on its own, and the small-M route that
+    W8A16Linear takes (the decode-step projection kernel in 16-row slices for
+    the shapes it serves, else the GEMV kernel), against the oracle."""
+    from src.quant_linear import w8a16_gemv_launch, w8a16_rows
+    from src.quant_utils import quantize_weight_symmetric_per_channel
+    w = _weights(N, K, torch.bfloat16, "normal", 7).to(dev)
+    q, s = quantize_weight_symmetric_per_channel(w)
+    x = torch.randn(M, K, generator=torch.Generator("cpu").manual_seed(8)).to(torch.bfloat16).to(dev)
+    ref = oq.w8a16(x, q, s)
+    scale = float(ref.float().abs().max()) + 1e-6
+    assert max_abs(w8a16_gemv_launch(x, q, s), ref) / scale < 2e-2
+    assert max_abs(w8a16_rows(x, q, s), ref) / scale < 2e-2
