@@ -206,14 +206,19 @@ __global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
                 (int64_t)kvh * a.v_sh + li * EPC;
   const uint8_t* mb =
       a.mask != nullptr ? a.mask + (int64_t)b * a.mask_sb : nullptr;
-  const int step = U * nw * RPW;
   const int my_off = w * RPW + rg;
 
-  for (int base = start; base < end; base += step) {
-    u32x4 kr[U][CPL], vr[U][CPL];
-    int row[U];
+  // One pass over UU row groups per wave (UU * nw * RPW keys from `base`).
+  // Full passes of U groups cover the split; a remainder of at most two
+  // groups runs in one-group passes (so a split just past a multiple of the
+  // U-group step does not pay a whole U-group pass for a few keys), a longer
+  // one in one more U-group pass (one round trip instead of up to U).
+  auto pass = [&](auto uu_c, const int base) __attribute__((always_inline)) {
+    constexpr int UU = decltype(uu_c)::value;
+    u32x4 kr[UU][CPL], vr[UU][CPL];
+    int row[UU];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < UU; ++u) {
       row[u] = base + u * nw * RPW + my_off;
       // Rows past `end` re-read the last valid row (always in bounds, never a
       // key beyond seq_lens) and are masked out of the softmax below.
@@ -223,16 +228,16 @@ __global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
         kr[u][j] = load16_stream(kb + rl * a.k_sl + j * LPR * EPC);
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < UU; ++u) {
       const int64_t rl = min(row[u], end - 1);
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
         vr[u][j] = load16_stream(vb + rl * a.v_sl + j * LPR * EPC);
     }
 
-    float s[U][GC];
+    float s[UU][GC];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < UU; ++u) {
       bool keep = row[u] < end;
       if (mb != nullptr && keep) keep = mb[(int64_t)row[u] * a.mask_sl] != 0;
 #pragma unroll
@@ -245,18 +250,18 @@ __global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
       }
     }
 
-    float p[U][GC];
+    float p[UU][GC];
 #pragma unroll
     for (int g = 0; g < GC; ++g) {
       float mx = s[0][g];
 #pragma unroll
-      for (int u = 1; u < U; ++u) mx = fmaxf(mx, s[u][g]);
+      for (int u = 1; u < UU; ++u) mx = fmaxf(mx, s[u][g]);
       const float mn = fmaxf(m[g], mx);
       const float alpha = fast_exp2(m[g] - mn);
       m[g] = mn;
       float ls = 0.f;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
+      for (int u = 0; u < UU; ++u) {
         p[u][g] = fast_exp2(s[u][g] - mn);
         ls += p[u][g];
       }
@@ -266,7 +271,7 @@ __global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
     }
 
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < UU; ++u) {
       float vf[E];
 #pragma unroll
       for (int j = 0; j < CPL; ++j) Chunk<T>::unpack(vr[u][j], vf + j * EPC);
@@ -275,6 +280,14 @@ __global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
         for (int e = 0; e < E; ++e) acc[g][e] = fmaf(p[u][g], vf[e], acc[g][e]);
     }
+  };
+  const int grp = nw * RPW, step = U * grp;
+  int base = start;
+  for (; base + step <= end; base += step) pass(std::integral_constant<int, U>{}, base);
+  if (end - base > 2 * grp) {
+    pass(std::integral_constant<int, U>{}, base);
+  } else {
+    for (; base < end; base += grp) pass(std::integral_constant<int, 1>{}, base);
   }
 
   // Merge the RPW row groups of this wave (butterfly over lane strides).
