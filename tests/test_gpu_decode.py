@@ -172,3 +172,28 @@ def test_config4_long_context(dev, num_splits):
     ref, ref_lse = ora.decode(q, k, v)
     assert max_abs(out, ref) < 2e-2
     assert max_abs(lse, ref_lse) < LSE_TOL
+
+
+@pytest.mark.parametrize("D,base,rems", [
+    (64, 1024, (0, 1, 127, 128, 129, 256, 257, 300, 511)),   # one block: 16 waves x 8 rows
+    (128, 512, (0, 1, 63, 64, 65, 128, 129, 200, 255)),      # 16 waves x 4 rows
+])
+def test_split_pass_remainders(dev, D, base, rems):
+    """Key ranges that end exactly on a 4-row-group pass, one or two groups
+    past it (finished in one-group passes) and more (one more clamped pass):
+    every branch of the split loop against the oracle, with NaN in every slot
+    at or past the length so that any read beyond it would show."""
+    B, Hq, Hkv = len(rems), 4, 1
+    T = base + 512
+    q, k, v = _inputs(B, Hq, Hkv, T, D, torch.bfloat16, dev, seed=11)
+    lens = torch.tensor([base + r for r in rems], dtype=torch.int64)
+    k, v = k.clone(), v.clone()
+    for b in range(B):
+        k[b, :, lens[b]:] = float("nan")
+        v[b, :, lens[b]:] = float("nan")
+    for splits in (1, 3):
+        out, lse = _fd()(q, k, v, seq_lens=lens.to(dev), num_splits=splits, return_lse=True)
+        ref, ref_lse = ora.decode(q, k, v, seq_lens=lens)
+        assert not torch.isnan(out).any(), (D, splits)
+        assert max_abs(out, ref) < 2e-2, (D, splits)
+        assert max_abs(lse, ref_lse) < LSE_TOL, (D, splits)
