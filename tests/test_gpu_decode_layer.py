@@ -33,7 +33,8 @@ def _close(a, b, tol):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,K,N", [(1, 512, 384), (3, 2048, 512), (8, 2048, 2048), (16, 1024, 256),
-                                   (8, 8192, 2048), (12, 2048, 4096), (5, 3072, 600)])
+                                   (8, 8192, 2048), (12, 2048, 4096), (5, 3072, 600),
+                                   (7, 1024, 100), (2, 4096, 36)])
 @pytest.mark.parametrize("norm", [False, True])
 def test_linear_store_and_residual(dev, dtype, M, K, N, norm):
     if norm and (M * K * 2 > 64 * 1024 or (M > 8 and K > 2048)):
@@ -51,7 +52,8 @@ def test_linear_store_and_residual(dev, dtype, M, K, N, norm):
     _close(y, ref, 2e-2)
     _close(yr, (res.cpu().float() + ref.float()).to(dtype), 2e-2)
     # the unfused GPU chain (RMSNorm kernel, GEMV kernel, torch add)
-    un = lin(rmsnorm_triton(x, nw, 1e-5) if norm else x)
+    from src.quant_linear import w8a16_gemv_launch
+    un = w8a16_gemv_launch(rmsnorm_triton(x, nw, 1e-5) if norm else x, lin.weight, lin.scales)
     _close(y, un, 1e-2)
     _close(yr, res + un, 1e-2)
 
