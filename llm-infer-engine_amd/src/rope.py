@@ -113,9 +113,17 @@ def rope_and_cache_update(xk, xv, rope_cos, rope_sin, kv_cache, layer_idx,
     rope_sin are full tables indexed by the absolute slot position.
     """
     B, n_kv_heads, input_len, head_dim = xk.shape
-    _lib.require_device(xk, "rope_and_cache_update")
     if xv.shape != xk.shape:
         raise ValueError(f"xk and xv shapes must match, got {tuple(xk.shape)} and {tuple(xv.shape)}")
+    # the kernel writes B x n_kv_heads x head_dim slabs of layer layer_idx: a
+    # shape the cache does not hold would land in the next layer or past the end
+    if (B > kv_cache.max_batch_size or n_kv_heads != kv_cache.n_kv_heads
+            or head_dim != kv_cache.head_dim):
+        raise ValueError(f"xk/xv shape {tuple(xk.shape)} does not fit the cache "
+                         f"[{kv_cache.max_batch_size}, {kv_cache.n_kv_heads}, *, {kv_cache.head_dim}]")
+    if not -kv_cache.k.shape[0] <= layer_idx < kv_cache.k.shape[0]:
+        raise ValueError(f"layer_idx {layer_idx} out of range for a cache of {kv_cache.k.shape[0]} layers")
+    _lib.require_device(xk, "rope_and_cache_update")
     if scatter_positions is None and start_pos is None:
         raise ValueError("rope_and_cache_update needs start_pos or scatter_positions")
     if not cos_by_position:

@@ -21,6 +21,8 @@ How each part is pinned (see tests/test_oracle_*.py):
   quant               hand-built rows (zeros, ties, +-amax), |q| <= 127.
   linear              integer-exact cases computed with Python ints.
   norm                constant-row closed form.
-  model               composed from the pieces above (parity unpinned as a
-                      whole: no reference run or checkpoint exists offline).
+  model               transformers' LlamaForCausalLM (fp32, CPU) on the same
+                      checkpoint, token by token: logits within 1e-4 of scale,
+                      bf16 and W8A16 weights, default and llama3 RoPE, tied and
+                      untied heads; planted mistakes fail that bar.
 """

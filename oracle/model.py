@@ -5,8 +5,8 @@ src/model_quantized.py:42-190).  TEST INFRASTRUCTURE ONLY.
 Arithmetic is fp32; values are rounded to the activation dtype at the points
 where the engine stores them (after each projection, norm, RoPE, attention and
 residual add), so differences against the GPU come from summation order only.
-Parity of the composition as a whole is unpinned (no reference run or
-checkpoint offline); each piece is pinned by its own oracle tests.
+The composition is pinned against transformers' LlamaForCausalLM run on the
+same checkpoint in fp32 (tests/test_oracle_model.py).
 """
 from __future__ import annotations
 

@@ -83,3 +83,25 @@ def test_small_m_w8a16_routing_rule():
     assert not _fused_gemv_ok(torch.zeros(17, 2048, dtype=torch.bfloat16), w, s)
     assert not _fused_gemv_ok(x.float(), w, s.float())                    # fp32 x
     assert not _fused_gemv_ok(torch.zeros(2048, 8, dtype=torch.bfloat16).t(), w, s)  # k stride
+
+
+@pytest.mark.parametrize("shape,layer,msg", [
+    ((3, 2, 1, 16), 0, "does not fit the cache"),     # batch above max_batch_size
+    ((2, 3, 1, 16), 0, "does not fit the cache"),     # more kv heads than the cache
+    ((2, 1, 1, 16), 0, "does not fit the cache"),     # fewer kv heads (slot stride differs)
+    ((2, 2, 1, 32), 0, "does not fit the cache"),     # wider head_dim
+    ((2, 2, 1, 8), 0, "does not fit the cache"),      # narrower head_dim
+    ((2, 2, 1, 16), 2, "layer_idx 2 out of range"),   # past the last layer
+])
+def test_rope_and_cache_update_rejects_shapes_the_cache_does_not_hold(shape, layer, msg):
+    """Checked before anything launches (the kernel would otherwise write into
+    the next layer's slabs or past the allocation, src/rope.py:255-313)."""
+    from src.config import ModelArgs
+    from src.kv_cache import KVCache
+    from src.rope import rope_and_cache_update
+    args = ModelArgs(dim=64, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=32, max_batch_size=2,
+                     max_seq_len=8, device="cpu")
+    kv = KVCache(args, dtype=torch.bfloat16)
+    cos = torch.ones(1, shape[3] // 2, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match=msg):
+        rope_and_cache_update(_t(*shape), _t(*shape), cos, cos, kv, layer, start_pos=0)

@@ -27,13 +27,19 @@ def _small_model(args, quantized=False):
     return Llama3(args).to(args.device, torch.bfloat16).eval()
 
 
-def _logit_check(a, b):
+def _logit_check(a, b, tol_frac=2e-2):
+    """Logits within tol_frac of the oracle's logit scale; the engine's top-1
+    token equals the oracle's wherever the oracle's top-2 gap exceeds that
+    tolerance (closer pairs may swap under summation-order differences)."""
     a, b = a.float().cpu().reshape(-1, a.shape[-1]), b.float().cpu().reshape(-1, b.shape[-1])
     scale = float(b.abs().max())
-    assert max_abs(a, b) < 3e-2 * scale, (max_abs(a, b), scale)
-    # top-1 agreement up to near-ties: the oracle's logit at the engine's
-    # argmax is within the tolerance of the oracle's maximum
-    tol = 3e-2 * scale
+    tol = tol_frac * scale
+    err = max_abs(a, b)
+    print(f"logits: max|engine-oracle| = {err:.4e} = {err / scale:.3e} of scale {scale:.3f}")
+    assert err < tol, (err, scale)
+    top2 = b.topk(2, dim=-1).values
+    decisive = (top2[:, 0] - top2[:, 1]) > tol
+    assert torch.equal(a.argmax(-1)[decisive], b.argmax(-1)[decisive])
     picked = b.gather(1, a.argmax(-1, keepdim=True))[:, 0]
     assert bool((picked >= b.max(-1).values - tol).all())
 
