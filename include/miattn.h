@@ -113,6 +113,31 @@ int32_t mi_flash_decode(const void* q, const void* k, const void* v,
                         void* stream);
 
 /*
+ * mi_flash_decode without a caller workspace: the same kernels, with the split
+ * partials kept in a library-owned device array of
+ * MI_DECODE_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends).  It
+ * calls no hipMalloc/hipFree and allocates nothing, for callers that cannot
+ * allocate (code under graph capture, serving loops that forbid allocation).
+ * No counterpart in the reference.  The partials need
+ * batch*n_heads*num_splits*(head_dim+2)*4 bytes (each array rounded up to 256
+ * bytes); larger calls return MI_ERR_UNSUPPORTED before launching anything.
+ * Every call on one GPU shares that GPU's array: calls that overlap in time on
+ * one device (different streams, or host threads) race and must not be issued.
+ * num_splits == 1 uses no scratch.
+ */
+#define MI_DECODE_NOALLOC_SCRATCH_BYTES (16u << 20)
+int32_t mi_flash_decode_noalloc(const void* q, const void* k, const void* v,
+                                const uint8_t* mask, int64_t mask_sb, int64_t mask_sl,
+                                const int64_t* seq_lens, void* out, float* lse,
+                                int64_t batch, int64_t n_heads, int64_t n_kv_heads,
+                                int64_t kv_len, int64_t head_dim, int64_t num_splits,
+                                int64_t q_sb, int64_t q_sh, int64_t q_sd, int64_t k_sb,
+                                int64_t k_sh, int64_t k_sl, int64_t v_sb, int64_t v_sh,
+                                int64_t v_sl, int64_t o_sb, int64_t o_sh, int64_t o_sd,
+                                float sm_scale, int32_t empty_rows_nan, int32_t dtype,
+                                void* stream);
+
+/*
  * Split count the library would pick for a decode of this shape on the
  * current device (used when the caller passes no explicit num_splits).
  */

@@ -22,9 +22,16 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
+
+// Workspace of mi_flash_decode_noalloc: the split partials (acc, m, l) of one
+// call, for callers that cannot allocate.  Each device holds its own copy for
+// the life of the process; host code reaches it only through the address
+// hipGetSymbolAddress returns for the current device (scratch_base below).
+static __device__ __align__(256) unsigned char scratch[MI_DECODE_NOALLOC_SCRATCH_BYTES];
 
 namespace mi {
 
@@ -684,6 +691,35 @@ hipError_t launch_combine_any(int32_t dtype, const CombineArgs& c, int64_t B,
 
 constexpr int64_t kMaxSplits = 8192;
 
+// Device address of `scratch` on the current device, looked up once per device.
+int32_t scratch_base(unsigned char** out) {
+  static std::mutex mu;
+  static unsigned char* base[64] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_last_error("flash_decode_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return (int32_t)e;
+  }
+  if (dev < 0 || dev >= 64) {
+    set_last_error("flash_decode_noalloc: device %d out of range", dev);
+    return MI_ERR_UNSUPPORTED;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (base[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_last_error("flash_decode_noalloc: hipGetSymbolAddress(scratch) failed: %s",
+                     hipGetErrorString(e));
+      return e != hipSuccess ? (int32_t)e : MI_ERR_INVALID;
+    }
+    base[dev] = static_cast<unsigned char*>(p);
+  }
+  *out = base[dev];
+  return MI_OK;
+}
+
 }  // namespace
 }  // namespace mi
 
@@ -845,4 +881,49 @@ extern "C" int32_t mi_flash_decode(
     return (int32_t)e;
   }
   return MI_OK;
+}
+
+extern "C" int32_t mi_flash_decode_noalloc(
+    const void* q, const void* k, const void* v, const uint8_t* mask,
+    int64_t mask_sb, int64_t mask_sl, const int64_t* seq_lens, void* out, float* lse,
+    int64_t batch, int64_t n_heads, int64_t n_kv_heads, int64_t kv_len, int64_t head_dim,
+    int64_t num_splits, int64_t q_sb, int64_t q_sh, int64_t q_sd, int64_t k_sb,
+    int64_t k_sh, int64_t k_sl, int64_t v_sb, int64_t v_sh, int64_t v_sl,
+    int64_t o_sb, int64_t o_sh, int64_t o_sd, float sm_scale,
+    int32_t empty_rows_nan, int32_t dtype, void* stream) {
+  if (batch <= 0 || n_heads <= 0 || num_splits <= 0 || head_dim <= 0 ||
+      num_splits > kMaxSplits) {
+    set_last_error("flash_decode_noalloc: sizes must be positive and num_splits <= %lld",
+                   (long long)kMaxSplits);
+    return MI_ERR_INVALID;
+  }
+  if (num_splits == 1)  // single pass: no partials at all
+    return mi_flash_decode(q, k, v, mask, mask_sb, mask_sl, seq_lens, nullptr, nullptr,
+                           nullptr, out, lse, batch, n_heads, n_kv_heads, kv_len, head_dim,
+                           1, q_sb, q_sh, q_sd, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl, o_sb,
+                           o_sh, o_sd, sm_scale, empty_rows_nan, dtype, stream);
+  // layout in scratch: acc [B*Hq*S*D] fp32, then m and l [B*Hq*S] fp32 each,
+  // every array starting on a 256-byte boundary
+  const int64_t rows = batch * n_heads * num_splits;
+  auto up = [](int64_t b) { return (b + 255) & ~(int64_t)255; };
+  const int64_t acc_bytes = up(rows * head_dim * 4), ml_bytes = up(rows * 4);
+  if (head_dim > 1024 || rows > (int64_t)MI_DECODE_NOALLOC_SCRATCH_BYTES ||
+      acc_bytes + 2 * ml_bytes > (int64_t)MI_DECODE_NOALLOC_SCRATCH_BYTES) {
+    set_last_error("flash_decode_noalloc: partials of batch*n_heads*num_splits = %lld rows x "
+                   "(head_dim %lld + 2) fp32 exceed the %lld-byte scratch; use fewer splits "
+                   "or mi_flash_decode with a workspace",
+                   (long long)rows, (long long)head_dim,
+                   (long long)MI_DECODE_NOALLOC_SCRATCH_BYTES);
+    return MI_ERR_UNSUPPORTED;
+  }
+  unsigned char* base = nullptr;
+  int32_t st = scratch_base(&base);
+  if (st != MI_OK) return st;
+  float* part_acc = reinterpret_cast<float*>(base);
+  float* part_m = reinterpret_cast<float*>(base + acc_bytes);
+  float* part_l = reinterpret_cast<float*>(base + acc_bytes + ml_bytes);
+  return mi_flash_decode(q, k, v, mask, mask_sb, mask_sl, seq_lens, part_m, part_l, part_acc,
+                         out, lse, batch, n_heads, n_kv_heads, kv_len, head_dim, num_splits,
+                         q_sb, q_sh, q_sd, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl, o_sb, o_sh,
+                         o_sd, sm_scale, empty_rows_nan, dtype, stream);
 }

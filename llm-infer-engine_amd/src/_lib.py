@@ -68,6 +68,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i64, _i64, _i64,                      # o strides
         _f32, _i32, _i32, _ptr,                # sm_scale empty_nan dtype stream
     ]),
+    "mi_flash_decode_noalloc": (_i32, [
+        _ptr, _ptr, _ptr,
+        _ptr, _i64, _i64,
+        _ptr,
+        _ptr, _ptr,                            # out lse
+        _i64, _i64, _i64, _i64, _i64, _i64,
+        _i64, _i64, _i64,
+        _i64, _i64, _i64,
+        _i64, _i64, _i64,
+        _i64, _i64, _i64,                      # o strides
+        _f32, _i32, _i32, _ptr,                # sm_scale empty_nan dtype stream
+    ]),
     "mi_decode_default_splits": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "mi_attn_prefill": (_i32, [
         _ptr, _ptr, _ptr, _ptr, _ptr,          # q k v out lse
