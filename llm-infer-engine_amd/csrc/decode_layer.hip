@@ -98,6 +98,25 @@ __device__ inline V8 i8x8_cvt(uint32_t lo, uint32_t hi) {
 
 __device__ inline float silu_f32(float a) { return a / (1.0f + expf(-a)); }
 
+// x from lane (lane ^ OFF) without LDS traffic: a DPP row rotate for 8 (a
+// 16-lane row rotated by 8 is the xor), the gfx950 permlane swaps for 16 and 32.
+template <int OFF>
+__device__ inline float dl_lane_xor(float x, int lane) {
+  if constexpr (OFF == 8) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, true));
+  } else if constexpr (OFF == 16) {
+    auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                               false);
+    return __uint_as_float((lane & 16) ? sw[0] : sw[1]);
+  } else {
+    static_assert(OFF == 32, "lane stride");
+    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                               false);
+    return __uint_as_float((lane & 32) ? sw[0] : sw[1]);
+  }
+}
+
 // Weight row of tile row r (0..15) for tile `tile`: rows 0..RPB-1 of the tile;
 // for the RoPE epilogue a tile holds 8 rotation pairs: rows i and i+8 are head
 // dims d and d + D/2.
@@ -383,6 +402,262 @@ __global__ __launch_bounds__(64 * NW) void layer_gemv_kernel(LayerGemvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Diagonal-packed GEMV for M <= 8 token rows.
+//
+// One v_mfma_f32_16x16x32 multiplies a 16 x 32 A tile by a 32 x 16 B tile.
+// With at most 8 token rows half of B's columns would be padding, and an
+// 8-row weight tile half of A's rows; padding lanes still cost the CU's
+// vector-memory issue (about 64 bytes per clock per CU, the limit of these
+// small GEMVs once the weight stream is in flight).  Here both halves carry
+// data: A lanes of rows r < 8 hold weight row n(r) over the first 64 k of a
+// 128-k superchunk, rows r >= 8 the same weight rows over the second 64 k; B
+// columns c < 8 hold token row c over the first 64 k, columns c >= 8 token row
+// c - 8 over the second.  C[r][c] + C[r + 8][c + 8] (r, c < 8) is then the
+// 128-k dot product and the off-diagonal quadrants are discarded: every byte
+// loaded is used.
+//
+// A block has NW waves splitting K (SC consecutive superchunks each, K =
+// 128 * NW * SC) and owns TPB 8-row tiles of each of its NMAT matrices.  With
+// the RMSNorm prologue each wave normalises its own x slice in registers (the
+// row statistics meet once in LDS).  Each wave folds its diagonal quadrants
+// in registers, the waves' sums meet in LDS, and one thread per (token row,
+// output row) sums them and runs the epilogue.
+template <typename T, int NW, int SC, bool NORM, int EPI, int TPB>
+__global__ __launch_bounds__(64 * NW) void dgemv_kernel(LayerGemvArgs a) {
+  using MM = LMfma<T>;
+  typedef typename MM::v8 v8;
+  constexpr int NMAT = EPI == kEpiSwiglu ? 2 : 1;
+  constexpr int NT = NMAT * TPB;                       // 8-row A tiles per block
+  constexpr int RB = 8 * TPB;                          // output rows per block (per matrix)
+  constexpr int NOUT = EPI == kEpiQkvRope ? 64 : 8 * RB;  // epilogue threads
+  static_assert(NOUT <= 64 * NW, "too few threads for the epilogue");
+  __shared__ __align__(16) float red[NT][8][8][NW];    // [tile][row][token][wave]
+  __shared__ float ssq[NORM ? NW : 1][8];              // per-wave sums of squares
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  const int rr = r16 & 7;                // A: tile row / B: token row
+  const int kofs = (r16 >> 3) * 64 + 16 * g;
+  const bool m_ok = rr < a.M;
+  const int kw = w * SC * 128;
+
+  // ---- which matrix / tiles this block owns
+  int mat0 = 0, tile0 = blockIdx.x * TPB;
+  if constexpr (EPI == kEpiQkvRope) {
+    tile0 = blockIdx.x;
+    if (tile0 >= a.n_tiles0) {
+      tile0 -= a.n_tiles0;
+      mat0 = 1;
+      if (tile0 >= a.n_tiles1) { tile0 -= a.n_tiles1; mat0 = 2; }
+    }
+  }
+  const int half = a.D >> 1, tph = EPI == kEpiQkvRope ? half >> 2 : 1;
+  // weight row of tile row `row` of tile `tim` of the matrix: the QKV tiles hold
+  // 4 rotation pairs (rows 0..3 dims d, rows 4..7 dims d + D/2)
+  auto w_row = [&](int tim, int row) -> int {
+    if constexpr (EPI == kEpiQkvRope) {
+      const int head = tim / tph, j = tim - head * tph;
+      return head * a.D + 4 * j + (row & 3) + ((row >> 2) ? half : 0);
+    } else {
+      return tim * 8 + row;
+    }
+  };
+  const int8_t* wm0 = mat0 == 0 ? a.w0 : (mat0 == 1 ? a.w1 : a.w2);
+  const int64_t wsn0 = mat0 == 0 ? a.w_sn0 : (mat0 == 1 ? a.w_sn1 : a.w_sn2);
+  const int nvalid = EPI == kEpiQkvRope ? (mat0 == 0 ? a.Hq : a.Hkv) * a.D : a.N;
+  // weight rows through buffer resources (host-checked: each matrix spans
+  // < 2^31 bytes); rows past N get an out-of-range offset and load zeros
+  buf_rsrc wr[NMAT];
+  wr[0] = make_rsrc(wm0, (uint32_t)((int64_t)(nvalid - 1) * wsn0 + a.K));
+  if constexpr (NMAT == 2) wr[1] = make_rsrc(a.w1, (uint32_t)((int64_t)(a.N - 1) * a.w_sn1 + a.K));
+  uint32_t woff[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int n = w_row(tile0 + (t % TPB), rr);
+    const int64_t sn = t / TPB == 0 ? wsn0 : a.w_sn1;
+    woff[t] = n < nvalid ? (uint32_t)((int64_t)n * sn) : kOobOffset;
+  }
+
+  // ---- B operand (token rows through a buffer resource: rows >= M read zeros
+  //      without a memory access), then the norm weights, then every weight
+  //      load of this wave; all issued before the first wait
+  const buf_rsrc xrs =
+      make_rsrc(a.x, (uint32_t)(((int64_t)(a.M - 1) * a.x_sm + a.K) * sizeof(T)));
+  const uint32_t xo = m_ok ? (uint32_t)((int64_t)rr * a.x_sm * sizeof(T)) : kOobOffset;
+  u32x4 xr[SC][2];
+#pragma unroll
+  for (int s = 0; s < SC; ++s) {
+    const int k0 = kw + s * 128 + kofs;
+    xr[s][0] = buf_load16(xrs, xo + (uint32_t)(k0 * sizeof(T)));
+    xr[s][1] = buf_load16(xrs, xo + (uint32_t)((k0 + 8) * sizeof(T)));
+  }
+  u32x4 nr[NORM ? SC : 1][2];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int s = 0; s < SC; ++s) {
+      const T* np = reinterpret_cast<const T*>(a.norm_w) + kw + s * 128 + kofs;
+      nr[s][0] = load16(np);
+      nr[s][1] = load16(np + 8);
+    }
+  }
+  u32x4 wq[NT][SC];
+#pragma unroll
+  for (int s = 0; s < SC; ++s)
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      wq[t][s] = buf_load16_nt(wr[t / TPB], woff[t] + (uint32_t)(kw + s * 128 + kofs));
+
+  // ---- epilogue operands, behind the weights (every thread loads from
+  //      clamped indices; only threads < NOUT use them)
+  const int et = tid % NOUT;
+  T e_s0, e_s1, e_res, e_cos, e_sin;
+  int64_t pos = 0;
+  if constexpr (EPI == kEpiQkvRope) {
+    pos = *a.pos;
+    const T* sc = reinterpret_cast<const T*>(mat0 == 0 ? a.s0 : (mat0 == 1 ? a.s1 : a.s2));
+    const int row = et & 7, j = tile0 % tph;
+    e_s0 = sc[w_row(tile0, row)];
+    e_s1 = sc[w_row(tile0, row ^ 4)];
+    const int64_t crow = min(max(pos - a.rope_row0, (int64_t)0), a.rope_rows - 1);
+    const int ii = 4 * j + (row & 3);
+    e_cos = reinterpret_cast<const T*>(a.cos)[crow * a.c_ss + ii];
+    e_sin = reinterpret_cast<const T*>(a.sin)[crow * a.c_ss + ii];
+  } else {
+    const int em = min(et / RB, a.M - 1);
+    const int en = min(blockIdx.x * RB + et % RB, a.N - 1);
+    e_s0 = reinterpret_cast<const T*>(a.s0)[en];
+    if constexpr (EPI == kEpiSwiglu) e_s1 = reinterpret_cast<const T*>(a.s1)[en];
+    if constexpr (EPI == kEpiResidual)
+      e_res = reinterpret_cast<const T*>(a.res)[(int64_t)em * a.res_sm + en];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- RMSNorm: per-token-row sum of squares over this lane's k (lanes c,
+  //      c ^ 8 and every k group share a token row), over waves in LDS; then
+  //      x * rstd * w rounded once to T, in place
+  if constexpr (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int s = 0; s < SC; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float v[8];
+        Chunk<T>::unpack(xr[s][h], v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+      }
+    ss += dl_lane_xor<8>(ss, lane);
+    ss += dl_lane_xor<16>(ss, lane);
+    ss += dl_lane_xor<32>(ss, lane);
+    if (lane < 8) ssq[w][lane] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) tot += ssq[ww][rr];
+    const float rstd = 1.0f / sqrtf(tot / (float)a.K + a.eps);
+#pragma unroll
+    for (int s = 0; s < SC; ++s)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float v[8], wn[8];
+        Chunk<T>::unpack(xr[s][h], v);
+        Chunk<T>::unpack(nr[s][h], wn);
+        typedef T t8 __attribute__((ext_vector_type(8)));
+        t8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = Elem<T>::from_f32(v[e] * rstd * wn[e]);
+        xr[s][h] = __builtin_bit_cast(u32x4, o);
+      }
+  }
+
+  // ---- MFMAs over the wave's superchunks
+  f32x4 acc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < SC; ++s) {
+    const v8 xb0 = __builtin_bit_cast(v8, xr[s][0]);
+    const v8 xb1 = __builtin_bit_cast(v8, xr[s][1]);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      acc[t] = MM::mma(i8x8_cvt<T, v8>(wq[t][s].x, wq[t][s].y), xb0, acc[t]);
+      acc[t] = MM::mma(i8x8_cvt<T, v8>(wq[t][s].z, wq[t][s].w), xb1, acc[t]);
+    }
+  }
+
+  // ---- fold the diagonal quadrants: lane c + 16 g (g < 2, c < 8) holds
+  //      C[4g + i][c], lane + 40 holds C[4g + i + 8][c + 8]
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = acc[t][i] + dl_lane_xor<8>(dl_lane_xor<32>(acc[t][i], lane), lane);
+      if (g < 2 && r16 < 8) red[t][4 * g + i][r16][w] = v;
+    }
+  }
+  __syncthreads();
+  if (tid >= NOUT) return;
+
+  // sum over waves of tile t, row `row`, token row `mm`
+  auto wsum = [&](int t, int row, int mm) -> float {
+    const f32x4* p = reinterpret_cast<const f32x4*>(&red[t][row][mm][0]);
+    float acc_s = 0.f;
+#pragma unroll
+    for (int q = 0; q < NW / 4; ++q) {
+      const f32x4 v = p[q];
+      acc_s += v[0] + v[1] + v[2] + v[3];
+    }
+    return acc_s;
+  };
+  auto f32_of = [](T v) { return Elem<T>::to_f32(v); };
+  auto rnd = [](float v) { return Elem<T>::to_f32(Elem<T>::from_f32(v)); };
+
+  if constexpr (EPI == kEpiQkvRope) {
+    const int mm = tid >> 3, row = tid & 7;
+    if (mm >= a.M) return;
+    const float yv = rnd(wsum(0, row, mm) * f32_of(e_s0));
+    const float yp = rnd(wsum(0, row ^ 4, mm) * f32_of(e_s1));
+    const bool hi = row >= 4;
+    const int head = tile0 / tph;
+    const int d = w_row(tile0, row) - head * a.D;
+    T out;
+    if (mat0 == 2) {
+      out = Elem<T>::from_f32(yv);                  // v: appended unrotated (bitwise)
+    } else {
+      const float cs = f32_of(e_cos), sn = f32_of(e_sin);
+      const float x1 = hi ? yp : yv, x2 = hi ? yv : yp;
+      T y1, y2;
+      {
+#pragma clang fp contract(off)
+        const float x1c = x1 * cs, x2s = x2 * sn, x2c = x2 * cs, x1s = x1 * sn;
+        y1 = Elem<T>::from_f32(x1c - x2s);
+        y2 = Elem<T>::from_f32(x2c + x1s);
+      }
+      out = hi ? y2 : y1;
+    }
+    if (mat0 == 0) {
+      reinterpret_cast<T*>(a.y)[((int64_t)mm * a.Hq + head) * a.D + d] = out;
+    } else if (pos >= 0 && pos < a.capacity) {
+      T* c = reinterpret_cast<T*>(mat0 == 1 ? a.ck : a.cv);
+      c[(int64_t)mm * a.c_sb + (int64_t)head * a.c_sh + pos * a.c_st + d] = out;
+    }
+  } else {
+    const int mm = tid / RB, j = tid - mm * RB;
+    const int n = blockIdx.x * RB + j;
+    if (mm >= a.M || n >= a.N) return;
+    float v = rnd(wsum(j >> 3, j & 7, mm) * f32_of(e_s0));
+    if constexpr (EPI == kEpiResidual) {
+      v = rnd(f32_of(e_res) + v);
+    } else if constexpr (EPI == kEpiSwiglu) {
+      const float b = rnd(wsum(TPB + (j >> 3), j & 7, mm) * f32_of(e_s1));
+      v = rnd(silu_f32(v)) * b;
+    }
+    reinterpret_cast<T*>(a.y)[(int64_t)mm * a.y_sm + n] = Elem<T>::from_f32(v);
+  }
+}
+
 namespace {
 
 template <typename T, int NW, bool NORM, int EPI, int RPB, int MR>
@@ -438,6 +713,54 @@ template <typename T, int EPI>
 hipError_t dispatch_tile(const LayerGemvArgs& a, hipStream_t st) {
   if (a.N / 16 >= 240) return dispatch_norm<T, EPI, 16>(a, (a.N + 15) / 16, st);
   return dispatch_norm<T, EPI, 8>(a, (a.N + 7) / 8, st);
+}
+
+// Diagonal-packed kernel (M <= 8): waves and superchunks per wave from K =
+// 128 * NW * SC, at most 16 waves.
+template <typename T, bool NORM, int EPI, int TPB, int NW, int SC>
+hipError_t launch_dg(const LayerGemvArgs& a, int n_blocks, hipStream_t st) {
+  hipLaunchKernelGGL((dgemv_kernel<T, NW, SC, NORM, EPI, TPB>), dim3((unsigned)n_blocks),
+                     dim3(64 * NW), 0, st, a);
+  return hipGetLastError();
+}
+
+template <typename T, bool NORM, int EPI, int TPB>
+hipError_t dispatch_dg_k(const LayerGemvArgs& a, int n_blocks, hipStream_t st) {
+  switch (a.K) {
+    case 512: return launch_dg<T, NORM, EPI, TPB, 4, 1>(a, n_blocks, st);
+    case 1024: return launch_dg<T, NORM, EPI, TPB, 8, 1>(a, n_blocks, st);
+    case 1536: return launch_dg<T, NORM, EPI, TPB, 12, 1>(a, n_blocks, st);
+    case 2048: return launch_dg<T, NORM, EPI, TPB, 16, 1>(a, n_blocks, st);
+    case 3072: return launch_dg<T, NORM, EPI, TPB, 12, 2>(a, n_blocks, st);
+    case 4096: return launch_dg<T, NORM, EPI, TPB, 16, 2>(a, n_blocks, st);
+    default: break;
+  }
+  if constexpr (EPI != kEpiSwiglu) {  // two weight streams: K <= 4096 (host-checked)
+    switch (a.K) {
+      case 6144: return launch_dg<T, NORM, EPI, TPB, 16, 3>(a, n_blocks, st);
+      case 8192: return launch_dg<T, NORM, EPI, TPB, 16, 4>(a, n_blocks, st);
+      default: break;
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
+template <typename T, int EPI, int TPB>
+hipError_t dispatch_dg(const LayerGemvArgs& a, int n_blocks, hipStream_t st) {
+  return a.norm_w != nullptr ? dispatch_dg_k<T, true, EPI, TPB>(a, n_blocks, st)
+                             : dispatch_dg_k<T, false, EPI, TPB>(a, n_blocks, st);
+}
+
+// Store / residual / SwiGLU projections: the diagonal-packed kernel for M <= 8
+// (one 8-row tile per block; SwiGLU two tiles of each matrix), else the
+// 16-column kernel above.
+template <typename T, int EPI>
+hipError_t dispatch_linear(const LayerGemvArgs& a, hipStream_t st) {
+  if (a.M <= 8) {
+    constexpr int TPB = EPI == kEpiSwiglu ? 2 : 1;
+    return dispatch_dg<T, EPI, TPB>(a, (a.N + 8 * TPB - 1) / (8 * TPB), st);
+  }
+  return dispatch_tile<T, EPI>(a, st);
 }
 
 bool k_supported(int64_t K) {
@@ -538,13 +861,13 @@ extern "C" int32_t mi_w8a16_linear_fused(
   hipStream_t s = (hipStream_t)stream;
   hipError_t e;
   if (dtype == MI_DTYPE_BF16) {
-    e = epilogue == kEpiStore ? dispatch_tile<bf16_t, kEpiStore>(a, s)
-        : epilogue == kEpiResidual ? dispatch_tile<bf16_t, kEpiResidual>(a, s)
-                                   : dispatch_tile<bf16_t, kEpiSwiglu>(a, s);
+    e = epilogue == kEpiStore ? dispatch_linear<bf16_t, kEpiStore>(a, s)
+        : epilogue == kEpiResidual ? dispatch_linear<bf16_t, kEpiResidual>(a, s)
+                                   : dispatch_linear<bf16_t, kEpiSwiglu>(a, s);
   } else {
-    e = epilogue == kEpiStore ? dispatch_tile<f16_t, kEpiStore>(a, s)
-        : epilogue == kEpiResidual ? dispatch_tile<f16_t, kEpiResidual>(a, s)
-                                   : dispatch_tile<f16_t, kEpiSwiglu>(a, s);
+    e = epilogue == kEpiStore ? dispatch_linear<f16_t, kEpiStore>(a, s)
+        : epilogue == kEpiResidual ? dispatch_linear<f16_t, kEpiResidual>(a, s)
+                                   : dispatch_linear<f16_t, kEpiSwiglu>(a, s);
   }
   if (e != hipSuccess) {
     set_last_error("%s: launch failed: %s", what, hipGetErrorString(e));
@@ -590,13 +913,24 @@ extern "C" int32_t mi_w8a16_qkv_rope_append(
   a.ck = cache_k; a.cv = cache_v; a.c_sb = c_sb; a.c_sh = c_sh; a.c_st = c_st;
   a.capacity = capacity;
   a.Hq = (int32_t)n_heads; a.Hkv = (int32_t)n_kv_heads; a.D = (int32_t)head_dim;
-  const int tph = (int)(head_dim / 16);   // tiles (8 rotation pairs each) per head
-  a.n_tiles0 = (int32_t)(n_heads * tph);
-  a.n_tiles1 = (int32_t)(n_kv_heads * tph);
-  const int n_blocks = a.n_tiles0 + 2 * a.n_tiles1;
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e = dtype == MI_DTYPE_BF16 ? dispatch_norm<bf16_t, kEpiQkvRope, 16>(a, n_blocks, s)
-                                        : dispatch_norm<f16_t, kEpiQkvRope, 16>(a, n_blocks, s);
+  hipError_t e;
+  if (M <= 8) {
+    // diagonal-packed kernel: 8-row tiles of 4 rotation pairs
+    const int tph = (int)(head_dim / 8);
+    a.n_tiles0 = (int32_t)(n_heads * tph);
+    a.n_tiles1 = (int32_t)(n_kv_heads * tph);
+    const int n_blocks = a.n_tiles0 + 2 * a.n_tiles1;
+    e = dtype == MI_DTYPE_BF16 ? dispatch_dg<bf16_t, kEpiQkvRope, 1>(a, n_blocks, s)
+                               : dispatch_dg<f16_t, kEpiQkvRope, 1>(a, n_blocks, s);
+  } else {
+    const int tph = (int)(head_dim / 16);   // tiles (8 rotation pairs each) per head
+    a.n_tiles0 = (int32_t)(n_heads * tph);
+    a.n_tiles1 = (int32_t)(n_kv_heads * tph);
+    const int n_blocks = a.n_tiles0 + 2 * a.n_tiles1;
+    e = dtype == MI_DTYPE_BF16 ? dispatch_norm<bf16_t, kEpiQkvRope, 16>(a, n_blocks, s)
+                               : dispatch_norm<f16_t, kEpiQkvRope, 16>(a, n_blocks, s);
+  }
   if (e != hipSuccess) {
     set_last_error("%s: launch failed: %s", what, hipGetErrorString(e));
     return (int32_t)e;
