@@ -383,18 +383,127 @@ struct CombineArgs {
   void* out;
   float* lse;
   int64_t o_sb, o_sh, o_sd;
+  int64_t n_rows;          // batch * n_heads
   int32_t n_heads, head_dim, num_splits;
   int32_t empty_nan;
 };
 
-// One workgroup per (batch, head): weights exp2(m_s - M) for splits with
+// Wave-wide reductions over all 64 lanes (DPP within rows of 16, permlane
+// swaps across them; no LDS).
+__device__ inline float wave_max(float x, int lane) {
+  x = group_max<16>(x);
+  x = fmaxf(x, lane_xor<16>(x, lane));
+  return fmaxf(x, lane_xor<32>(x, lane));
+}
+__device__ inline float wave_sum(float x, int lane) {
+  x = group_sum<16>(x);
+  x += lane_xor<16>(x, lane);
+  return x + lane_xor<32>(x, lane);
+}
+
+// One wave per (batch, head), four per workgroup: weights exp2(m_s - M) for
+// splits with l_s > 0 (src/flash_decode.py:182-192), numerator over splits in
+// float4 columns, out = num / max(den, 1) or 0 / NaN for empty rows
+// (src/flash_decode.py:203-205).  Latency-bound (a few KB per row): every
+// load of the first pass is issued before any reduction (one round trip to
+// the partials), and the reductions stay in registers -- no barrier.
+//   lanes: 64 = NSG split groups x (D / 4) column chunks
+template <typename T>
+__global__ __launch_bounds__(256) void decode_combine_wave_kernel(CombineArgs a) {
+  constexpr int kUnroll = 8;
+  const int lane = threadIdx.x & 63;
+  const int64_t bh = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (bh >= a.n_rows) return;
+  const int S = a.num_splits, D = a.head_dim;
+  const int b = (int)(bh / a.n_heads), h = (int)(bh % a.n_heads);
+  const float* pm = a.part_m + bh * S;
+  const float* pl = a.part_l + bh * S;
+  const float* pacc = a.part_acc + bh * S * D;
+  const int ncol = D >> 2;                   // float4 columns (<= 64)
+  const int nsg = 64 / ncol;                 // split groups
+  const int c = lane % ncol, sg = lane / ncol;
+
+  // first pass: (m, l) of split `lane`, and this lane's numerator columns of
+  // splits sg, sg + nsg, ... with their own (m, l)
+  const bool own = lane < S;
+  const float my_m = own ? pm[lane] : kNegBig;
+  const float my_l = own ? pl[lane] : 0.f;
+  f32x4 pv[kUnroll];
+  float pvm[kUnroll], pvl[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int sp = sg + u * nsg;
+    const bool ok = sp < S;
+    const int si = ok ? sp : 0;
+    pv[u] = *reinterpret_cast<const f32x4*>(pacc + (int64_t)si * D + 4 * c);
+    pvm[u] = pm[si];
+    pvl[u] = ok ? pl[si] : 0.f;
+  }
+
+  // max over non-empty splits, then the denominator
+  float mx = my_l > 0.f ? my_m : kNegBig;
+  for (int sp = lane + 64; sp < S; sp += 64)
+    if (pl[sp] > 0.f) mx = fmaxf(mx, pm[sp]);
+  const float M = wave_max(mx, lane);
+  float den = my_l > 0.f ? fast_exp2(my_m - M) * my_l : 0.f;
+  for (int sp = lane + 64; sp < S; sp += 64) {
+    const float ls = pl[sp];
+    if (ls > 0.f) den += fast_exp2(pm[sp] - M) * ls;
+  }
+  den = wave_sum(den, lane);
+
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u)
+    if (pvl[u] > 0.f) acc += fast_exp2(pvm[u] - M) * pv[u];
+  for (int s0 = sg + nsg * kUnroll; s0 < S; s0 += nsg * kUnroll) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int sp = s0 + u * nsg;
+      const bool ok = sp < S;
+      const int si = ok ? sp : 0;
+      pv[u] = *reinterpret_cast<const f32x4*>(pacc + (int64_t)si * D + 4 * c);
+      pvm[u] = pm[si];
+      pvl[u] = ok ? pl[si] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (pvl[u] > 0.f) acc += fast_exp2(pvm[u] - M) * pv[u];
+  }
+  // sum the split groups: lanes c, c + ncol, c + 2 ncol, ... hold the same columns
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float x = acc[i];
+    if (ncol <= 8) x += lane_xor<8>(x, lane);
+    if (ncol <= 16) x += lane_xor<16>(x, lane);
+    if (ncol <= 32) x += lane_xor<32>(x, lane);
+    acc[i] = x;
+  }
+  if (sg == 0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float o;
+      if (den > 0.f)
+        o = acc[i] / fmaxf(den, 1.0f);
+      else
+        o = a.empty_nan ? __builtin_nanf("") : 0.f;
+      T* op = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
+              (int64_t)(4 * c + i) * a.o_sd;
+      *op = Elem<T>::from_f32(o);
+    }
+  }
+  if (lane == 0 && a.lse != nullptr)
+    a.lse[bh] = den > 0.f ? (M + __log2f(den)) * kLn2 : -INFINITY;
+}
+
+// Many splits: one workgroup per (batch, head): weights exp2(m_s - M) for splits with
 // l_s > 0 (src/flash_decode.py:182-192), numerator over splits in float4
 // columns, out = num/den or 0/NaN for empty rows (src/flash_decode.py:203-205).
 // Latency-bound (a few KB per row): every thread issues all of its partial
 // loads (m, l and its first 8 numerator rows) before it reduces, so a call of
 // up to 256 splits costs one round trip to the partials, not one per split.
 template <typename T>
-__global__ __launch_bounds__(256) void decode_combine_kernel(CombineArgs a) {
+__global__ __launch_bounds__(256) void decode_combine_block_kernel(CombineArgs a) {
   constexpr int kUnroll = 8;
   extern __shared__ float smem[];
   __shared__ float red[2][4];
@@ -498,22 +607,28 @@ namespace {
 
 int elem_bytes(int32_t dtype) { return dtype == MI_DTYPE_F32 ? 4 : 2; }
 
-int gc_max(int32_t dtype, int64_t D) {
-  const int e_per_lane_chunks = (int)(D * elem_bytes(dtype) / 16);
-  const int lpr = e_per_lane_chunks < 16 ? e_per_lane_chunks : 16;
-  const int E = (e_per_lane_chunks / lpr) * (16 / elem_bytes(dtype));
-  return E <= 8 ? 4 : 2;
+// Host mirror of DecodeGeom: lanes per row, elements per lane, row unroll
+// and heads per block for a dtype / head_dim.
+struct HostGeom {
+  int lpr, e, rpw, u, gcmax;
+};
+HostGeom host_geom(int32_t dtype, int64_t D) {
+  const int eb = elem_bytes(dtype);
+  const int ch = (int)(D * eb / 16), epc = 16 / eb;
+  HostGeom g;
+  g.lpr = ch < 16 ? ch : 16;
+  g.e = (ch / g.lpr) * epc;
+  g.rpw = 64 / g.lpr;
+  g.u = g.e <= 8 ? 4 : 2;
+  g.gcmax = g.e <= 8 ? 4 : 2;
+  return g;
 }
+
+int gc_max(int32_t dtype, int64_t D) { return host_geom(dtype, D).gcmax; }
 
 bool supported_head_dim(int32_t dtype, int64_t D) {
   if (dtype == MI_DTYPE_F32) return D == 32 || D == 64 || D == 128 || D == 256;
   return D == 64 || D == 128 || D == 256 || D == 32;
-}
-
-int rows_per_wave_load(int32_t dtype, int64_t D) {
-  const int ch = (int)(D * elem_bytes(dtype) / 16);
-  const int lpr = ch < 16 ? ch : 16;
-  return 64 / lpr;
 }
 
 struct Plan {
@@ -536,9 +651,8 @@ Plan make_plan(int32_t dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
   else if (blocks < 2 * cus)
     nw = 8;
   // No more waves than the split has row-loads for.
-  const int rpw = rows_per_wave_load(dtype, D);
-  const int unroll = gc_max(dtype, D) == 4 ? 4 : 2;
-  while (nw > 1 && (int64_t)nw * rpw * unroll > p.split_len) nw >>= 1;
+  const HostGeom geo = host_geom(dtype, D);
+  while (nw > 1 && (int64_t)nw * geo.rpw * geo.u > p.split_len) nw >>= 1;
   p.nw = nw;
   return p;
 }
@@ -668,22 +782,40 @@ hipError_t launch_split_any(int32_t dtype, const DecodeArgs& a, const Plan& p,
   }
 }
 
+// Many rows with up to 16 splits each: one wave per (batch, head) row (no
+// barriers); otherwise one workgroup per row (the splits' loads spread over
+// 256 threads, which a few rows need to fill the GPU).
 hipError_t launch_combine_any(int32_t dtype, const CombineArgs& c, int64_t B,
                               int64_t Hq, hipStream_t stream) {
+  dim3 block(256);
+  if (c.num_splits <= 16 && B * Hq >= 64) {
+    dim3 grid((unsigned)((B * Hq + 3) / 4));
+    switch (dtype) {
+      case MI_DTYPE_BF16:
+        hipLaunchKernelGGL(decode_combine_wave_kernel<bf16_t>, grid, block, 0, stream, c);
+        break;
+      case MI_DTYPE_F16:
+        hipLaunchKernelGGL(decode_combine_wave_kernel<f16_t>, grid, block, 0, stream, c);
+        break;
+      default:
+        hipLaunchKernelGGL(decode_combine_wave_kernel<float>, grid, block, 0, stream, c);
+        break;
+    }
+    return hipGetLastError();
+  }
   const int D = c.head_dim;
   const int nsp = 256 / (D / 4);
   const size_t shmem = ((size_t)c.num_splits + (size_t)nsp * D) * sizeof(float);
   dim3 grid((unsigned)(B * Hq));
-  dim3 block(256);
   switch (dtype) {
     case MI_DTYPE_BF16:
-      hipLaunchKernelGGL(decode_combine_kernel<bf16_t>, grid, block, shmem, stream, c);
+      hipLaunchKernelGGL(decode_combine_block_kernel<bf16_t>, grid, block, shmem, stream, c);
       break;
     case MI_DTYPE_F16:
-      hipLaunchKernelGGL(decode_combine_kernel<f16_t>, grid, block, shmem, stream, c);
+      hipLaunchKernelGGL(decode_combine_block_kernel<f16_t>, grid, block, shmem, stream, c);
       break;
     default:
-      hipLaunchKernelGGL(decode_combine_kernel<float>, grid, block, shmem, stream, c);
+      hipLaunchKernelGGL(decode_combine_block_kernel<float>, grid, block, shmem, stream, c);
       break;
   }
   return hipGetLastError();
@@ -811,7 +943,7 @@ extern "C" int32_t mi_decode_combine(const float* part_m, const float* part_l,
                    (long long)num_splits, (long long)kMaxSplits);
     return MI_ERR_UNSUPPORTED;
   }
-  if (head_dim % 4 != 0 || head_dim > 1024 || (256 % (head_dim / 4)) != 0) {
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256) {
     set_last_error("decode_combine: head_dim %lld unsupported", (long long)head_dim);
     return MI_ERR_UNSUPPORTED;
   }
@@ -826,6 +958,7 @@ extern "C" int32_t mi_decode_combine(const float* part_m, const float* part_l,
   c.out = out;
   c.lse = lse;
   c.o_sb = o_sb; c.o_sh = o_sh; c.o_sd = o_sd;
+  c.n_rows = batch * n_heads;
   c.n_heads = (int32_t)n_heads;
   c.head_dim = (int32_t)head_dim;
   c.num_splits = (int32_t)num_splits;
