@@ -7,7 +7,7 @@ Headline (`value`): BASELINE config 2 — causal GQA prefill, bf16, B4 S2048
 4: B1 L=131072, split sweep) in GB/s, the W8A16 decode step (config 5) in
 tokens/s, and the W8A16 prefill GEMM (one layer's projections at config 2's
 8192 tokens) in TFLOP/s, each with its own roofline; and the CPU baseline (the
-fp32 oracle on the host cores, on a bounded sample).
+fp32 oracle on the host cores, one bounded sample per config, under each leg).
 
 A step is one flash_attention call on resident inputs.  Timing: untimed
 warm-up (at least W steps and at least 0.25 s of back-to-back steps, so the GPU
@@ -229,7 +229,8 @@ def bench_config5(torch, steps: int, warmup: int) -> dict:
            "roofline": {"bound": "hbm", "achieved": round(nbytes / (ms * 1e-3) / 1e9, 1),
                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                        "traffic": None}}
+                        "traffic": _traffic("decode_step_config5_traffic.md",
+                                            "hbm_bytes_per_step")}}
     del runner, model, kv
     torch.cuda.empty_cache()
     return out
@@ -345,29 +346,165 @@ def bench_loader(torch) -> dict:
     return out
 
 
-def cpu_baseline(torch) -> dict:
-    """The fp32 CPU oracle on batch 0 of config 2 (1/4 of a step), on rank 0."""
-    from oracle import attention as ora
-    threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
-    g = torch.Generator("cpu").manual_seed(0)
-    q = (torch.randn((4, 32, 2048, 64), generator=g) / 8.0).to(torch.bfloat16)[:1]
-    k = torch.randn((4, 8, 2048, 64), generator=g).to(torch.bfloat16)[:1]
-    v = torch.randn((4, 8, 2048, 64), generator=g).to(torch.bfloat16)[:1]
-    flops = 4.0 * 1 * 32 * 2048 * 2048 * 64 / 2
-    ora.prefill(q, k, v, sm_scale=1.0)
+def _cpu_threads(torch) -> dict:
+    """Use every CPU this process may run on (the lease's share of the host,
+    from the affinity mask) and record what the host offers."""
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        aff = os.cpu_count() or 1
+    torch.set_num_threads(aff)
+    return {"cpu": _cpu_name(), "os_cpu_count": os.cpu_count(), "affinity_cpus": aff,
+            "torch_threads": torch.get_num_threads()}
+
+
+def _cpu_median(fn, warm: int = 2, reps: int = 5) -> float:
+    """Median wall time of `reps` calls after `warm` untimed ones."""
+    for _ in range(warm):
+        fn()
     ts = []
-    for _ in range(3):
+    for _ in range(reps):
         t0 = time.perf_counter()
-        ora.prefill(q, k, v, sm_scale=1.0)
+        fn()
         ts.append(time.perf_counter() - t0)
     ts.sort()
-    t = ts[1]
-    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": f"oracle.prefill (torch fp32, CPU) on batch 0 of config 2 = 1/4 step "
-                      f"({flops/1e9:.2f} GFLOP), median of 3 after 1 warm-up: {t:.2f} s; "
-                      f"host {_cpu_name()}"}
+    return ts[len(ts) // 2]
+
+
+def _cpu_entry(value, unit, host, sample, t) -> dict:
+    return {"value": value, "unit": unit, "cores": host["torch_threads"], "kind": "port",
+            "sample": f"{sample}; median of 5 after 2 warm-ups: {t:.3f} s per call",
+            "host": host}
+
+
+def cpu_baselines(torch) -> dict:
+    """The fp32 CPU oracle (this build's restatement of the reference maths,
+    oracle/) on the host cores, one bounded sample per BASELINE config, each
+    scaled to that config's metric.  Inputs are bf16-rounded like the GPU legs'."""
+    from oracle import attention as ora
+    from oracle import quant as oq
+    from oracle import rope as orope
+    host = _cpu_threads(torch)
+    out = {}
+    g = torch.Generator("cpu").manual_seed(0)
+
+    # config 1: fp32 RoPE (theta 5e5) on Q and K + causal GQA prefill, B1 S512 32/8 D64
+    q = torch.randn((1, 32, 512, 64), generator=g)
+    k = torch.randn((1, 8, 512, 64), generator=g)
+    v = torch.randn((1, 8, 512, 64), generator=g)
+    cos, sin = orope.cos_sin(orope.freqs_cis(64, 512, 500000.0), torch.float32)
+    fl1 = 4.0 * 32 * 512 * 512 * 64 / 2
+    t = _cpu_median(lambda: ora.prefill(orope.rotate(q, cos, sin), orope.rotate(k, cos, sin), v))
+    out["config1"] = _cpu_entry(round(fl1 / t / 1e12, 5), "TFLOP/s", host,
+                                "config 1 whole (RoPE on Q/K + prefill, 1.074 GFLOP)", t)
+
+    # config 2: the whole step (B4 S2048 32/8 D64, fp32 LSE)
+    q = (torch.randn((4, 32, 2048, 64), generator=g) / 8.0).to(torch.bfloat16)
+    k = torch.randn((4, 8, 2048, 64), generator=g).to(torch.bfloat16)
+    v = torch.randn((4, 8, 2048, 64), generator=g).to(torch.bfloat16)
+    fl2 = 4.0 * 4 * 32 * 2048 * 2048 * 64 / 2
+    t = _cpu_median(lambda: ora.prefill(q, k, v, sm_scale=1.0))
+    out["config2"] = _cpu_entry(round(fl2 / t / 1e12, 4), "TFLOP/s", host,
+                                "config 2 whole step (68.72 GFLOP)", t)
+    del q, k, v
+
+    # config 3: the first 4 of the 16 sequences (their own lengths), bf16 K/V
+    g3 = torch.Generator("cpu").manual_seed(0)
+    lens = torch.randint(1024, 8193, (16,), generator=g3)[:4]
+    Lm = int(lens.max())
+    q = torch.randn((4, 24, 1, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((4, 8, Lm, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((4, 8, Lm, 128), generator=g).to(torch.bfloat16)
+    by3 = int(lens.sum()) * 8 * 128 * 2 * 2 + 2 * 4 * 24 * 128 * 2
+    t = _cpu_median(lambda: ora.decode(q, k, v, seq_lens=lens))
+    out["config3"] = _cpu_entry(round(by3 / t / 1e9, 2), "GB/s", host,
+                                f"config 3, sequences 0-3 (lengths {lens.tolist()}, "
+                                f"{by3 / 1e6:.1f} MB of bf16 K/V + q/o)", t)
+    del q, k, v
+
+    # config 4: a quarter of the context (32768 of 131072 keys)
+    q = torch.randn((1, 24, 1, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, 8, 32768, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((1, 8, 32768, 128), generator=g).to(torch.bfloat16)
+    by4 = 32768 * 8 * 128 * 2 * 2 + 2 * 24 * 128 * 2
+    t = _cpu_median(lambda: ora.decode(q, k, v))
+    out["config4"] = _cpu_entry(round(by4 / t / 1e9, 2), "GB/s", host,
+                                f"config 4 at 32768 of 131072 keys ({by4 / 1e6:.1f} MB)", t)
+    del q, k, v
+
+    # config 5: one of the 16 W8A16 layers (int8 weights dequantised q*s inside
+    # every call) and 1/16 of the bf16 lm_head rows; step = 16 x (layer + slice)
+    dim, hid, Hq, Hkv, D, B, pos = 2048, 8192, 32, 8, 64, 8, 4096
+
+    def w8(n, kk):
+        return (torch.randint(-127, 128, (n, kk), generator=g, dtype=torch.int8),
+                (torch.rand((n, 1), generator=g) * 2e-3 + 1e-3).to(torch.bfloat16))
+    wq, wk, wv, wo = w8(Hq * D, dim), w8(Hkv * D, dim), w8(Hkv * D, dim), w8(dim, Hq * D)
+    w1, w3, w2 = w8(hid, dim), w8(hid, dim), w8(dim, hid)
+    nw1 = torch.ones(dim, dtype=torch.bfloat16)
+    ck = torch.randn((B, Hkv, pos + 1, D), generator=g).to(torch.bfloat16)
+    cv = torch.randn((B, Hkv, pos + 1, D), generator=g).to(torch.bfloat16)
+    h0 = torch.randn((B, 1, dim), generator=g).to(torch.bfloat16)
+    lm = (torch.randn((128256 // 16, dim), generator=g) * 0.02).to(torch.bfloat16)
+    cs, sn = orope.cos_sin(orope.freqs_cis(D, pos + 1, 500000.0)[pos:pos + 1], torch.bfloat16)
+
+    def layer():
+        x = oq.rmsnorm(h0, nw1, 1e-5)
+        xq = oq.w8a16(x, *wq).view(B, 1, Hq, D).transpose(1, 2)
+        xk = oq.w8a16(x, *wk).view(B, 1, Hkv, D).transpose(1, 2)
+        xv = oq.w8a16(x, *wv).view(B, 1, Hkv, D).transpose(1, 2)
+        xq = orope.rotate(xq, cs, sn)
+        ck[:, :, pos] = orope.rotate(xk, cs, sn)[:, :, 0]
+        cv[:, :, pos] = xv[:, :, 0]
+        o, _ = ora.decode(xq, ck, cv)
+        h = (h0.float() + oq.w8a16(o.to(torch.bfloat16).transpose(1, 2).reshape(B, 1, dim),
+                                   *wo).float()).to(torch.bfloat16)
+        x = oq.rmsnorm(h, nw1, 1e-5)
+        a = oq.w8a16(x, *w1).float()
+        gg = (a * torch.sigmoid(a)).to(torch.bfloat16).float() * oq.w8a16(x, *w3).float()
+        return (h.float() + oq.w8a16(gg.to(torch.bfloat16), *w2).float()).to(torch.bfloat16)
+
+    def head():
+        x = oq.rmsnorm(h0, nw1, 1e-5)
+        return x.float() @ lm.float().t()
+    t_l = _cpu_median(layer)
+    t_h = _cpu_median(head)
+    t5 = 16 * (t_l + t_h)
+    out["config5"] = _cpu_entry(round(B / t5, 2), "tokens/s", host,
+                                f"config 5 from one W8A16 layer ({t_l:.3f} s, int8 -> fp32 "
+                                f"dequantisation inside) and 1/16 of the lm_head rows "
+                                f"({t_h:.3f} s), step = 16 x (layer + slice) = {t5:.2f} s", t_l)
+    return out
+
+
+def bench_prefill_cfg1(torch, steps: int, warmup: int) -> dict:
+    """Config 1 on the GPU (fp32 RoPE on Q and K + causal GQA prefill, B1 S512
+    32/8 D64): the parity configuration, timed beside its CPU baseline."""
+    from src.flash_attn import flash_attention
+    from src.rope import apply_rotary, build_rope_cos_sin, precompute_freqs_cis
+    dev = torch.device("cuda:0")
+    g = torch.Generator("cpu").manual_seed(0)
+    q = torch.randn((1, 32, 512, 64), generator=g).to(dev)
+    k = torch.randn((1, 8, 512, 64), generator=g).to(dev)
+    v = torch.randn((1, 8, 512, 64), generator=g).to(dev)
+    cos, sin = build_rope_cos_sin(precompute_freqs_cis(64, 512), torch.float32, dev)
+    flops = 4.0 * 32 * 512 * 512 * 64 / 2
+
+    def step():
+        return flash_attention(apply_rotary(q, cos, sin), apply_rotary(k, cos, sin), v,
+                               return_lse=True)
+    _settle(torch, step, warmup)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    return {"config": "1: fp32 RoPE (theta 5e5) on Q/K + causal GQA prefill B1 S512 32/8 D64",
+            "value": round(flops / (ms * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
+            "ms_per_step": ms, "flops": flops}
 
 
 def main() -> None:
@@ -403,6 +540,7 @@ def main() -> None:
     pre = None
     if args.only in (None, "prefill"):
         pre = bench_prefill(torch, args.steps, args.warmup)
+        extra["prefill_config1"] = bench_prefill_cfg1(torch, args.steps, args.warmup)
     if args.only in (None, "decode"):
         extra["decode_config3"] = bench_decode_cfg3(torch, args.steps, args.warmup)
         extra["decode_config4"] = bench_decode_cfg4(torch, args.steps, args.warmup)
@@ -414,7 +552,12 @@ def main() -> None:
         extra["checkpoint_load"] = bench_loader(torch)
     cpu = None
     if not args.no_cpu_baseline and args.only is None:
-        cpu = cpu_baseline(torch)
+        cpus = cpu_baselines(torch)
+        cpu = cpus["config2"]
+        for key, leg in (("config1", "prefill_config1"), ("config3", "decode_config3"),
+                         ("config4", "decode_config4"), ("config5", "decode_step_config5")):
+            if leg in extra:
+                extra[leg]["cpu_baseline"] = cpus[key]
     line = {
         "metric": "flash-decode HBM GB/s (% of peak) + prefill attn TFLOP/s, 1 MI355X",
         "value": round(pre["value"], 1) if pre else None,
