@@ -160,6 +160,12 @@ def bench_decode_cfg3(torch, steps: int, warmup: int) -> dict:
     graph = _graph_decode(torch, lambda i: flash_decode(qs[i], ks[i], vs[i], seq_lens=sl), n_sets)
     ms = _time_graph(torch, graph, n_sets, max(steps, 21), warmup)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    del graph
+    # the reference API's call (src/model.py:83): the same keys through a bool mask
+    mask = (torch.arange(8192)[None, :] < lens[:, None]).to(dev)
+    graph = _graph_decode(torch, lambda i: flash_decode(qs[i], ks[i], vs[i], mask=mask), n_sets)
+    ms_m = _time_graph(torch, graph, n_sets, max(steps, 21), warmup)
+    gbs_m = nbytes / (ms_m * 1e-3) / 1e9
     out = {
         "config": "3: decode B16 24/8 D128 T8192 L~U[1024,8192] (sum 96634), seq_lens, hipGraph",
         "value": round(gbs, 1), "unit": "GB/s", "ms_per_step": ms, "bytes": nbytes,
@@ -167,6 +173,9 @@ def bench_decode_cfg3(torch, steps: int, warmup: int) -> dict:
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": _traffic("decode_config3_4_traffic.md",
                                          "hbm_bytes_per_launch_config3")},
+        "mask_path": {"call": "flash_decode(q, k, v, mask=[16, 8192] bool = arange < L_b)",
+                      "value": round(gbs_m, 1), "unit": "GB/s", "ms_per_step": ms_m,
+                      "of_seq_lens_path": round(gbs_m / gbs, 3)},
     }
     del graph, ks, vs
     torch.cuda.empty_cache()

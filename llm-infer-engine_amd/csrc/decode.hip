@@ -136,8 +136,17 @@ struct DecodeGeom {
   static_assert(kCH % kLPR == 0, "chunks must split evenly across lanes");
 };
 
+// Mask bytes staged in LDS per window of rows (a longer split is processed in
+// windows of this many rows).
+constexpr int kMaskWin = 4096;
+
+// fp32 K/V at head_dim >= 128 hold twice the registers per row chunk: those
+// kernels run at most 8 waves (512 threads, 256 VGPRs), the others up to 16.
+template <typename T, int D>
+constexpr int split_max_threads() { return (sizeof(T) == 4 && D >= 128) ? 512 : 1024; }
+
 template <typename T, int D, int GC>
-__global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
+__global__ __launch_bounds__((split_max_threads<T, D>())) void decode_split_kernel(DecodeArgs a) {
   using Geo = DecodeGeom<T, D>;
   constexpr int EPC = Geo::kEPC, LPR = Geo::kLPR, CPL = Geo::kCPL,
                 E = Geo::kE, RPW = Geo::kRPW, U = Geo::kU;
@@ -214,6 +223,11 @@ __global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
   const uint8_t* mb =
       a.mask != nullptr ? a.mask + (int64_t)b * a.mask_sb : nullptr;
   const int my_off = w * RPW + rg;
+  // With a mask, the bytes of the current window of rows are staged in LDS
+  // (after the wave-merge area) so a pass knows which rows to fetch before it
+  // issues their loads: excluded rows are not streamed.
+  unsigned char* msk = reinterpret_cast<unsigned char*>(smem + nw * GC * (D + 2));
+  int wbase = start, wend = end;
 
   // One pass over UU row groups per wave (UU * nw * RPW keys from `base`).
   // Full passes of U groups cover the split; a remainder of at most two
@@ -227,33 +241,45 @@ __global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
       row[u] = base + u * nw * RPW + my_off;
-      // Rows past `end` re-read the last valid row (always in bounds, never a
-      // key beyond seq_lens) and are masked out of the softmax below.
-      const int64_t rl = min(row[u], end - 1);
+    }
+    // Rows past the window, and rows the mask excludes, re-read the window's
+    // last row (always in bounds, never a key beyond seq_lens: a cache hit,
+    // not a stream) and are dropped from the softmax below.
+    bool keep[UU];
+    int rl[UU];
+#pragma unroll
+    for (int u = 0; u < UU; ++u) {
+      keep[u] = row[u] < wend;
+      if (mb != nullptr && keep[u]) keep[u] = msk[row[u] - wbase] != 0;
+      // (fp32 K/V keep the plain clamp: the 1024-thread kernels have no
+      // registers to spare for the row selection)
+      rl[u] = sizeof(T) == 2 ? (keep[u] ? row[u] : wend - 1) : min(row[u], wend - 1);
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
-        kr[u][j] = load16_stream(kb + rl * a.k_sl + j * LPR * EPC);
+        kr[u][j] = load16_stream(kb + (int64_t)rl[u] * a.k_sl + j * LPR * EPC);
     }
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
-      const int64_t rl = min(row[u], end - 1);
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
-        vr[u][j] = load16_stream(vb + rl * a.v_sl + j * LPR * EPC);
+        vr[u][j] = load16_stream(vb + (int64_t)rl[u] * a.v_sl + j * LPR * EPC);
     }
 
     float s[UU][GC];
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
-      bool keep = row[u] < end;
-      if (mb != nullptr && keep) keep = mb[(int64_t)row[u] * a.mask_sl] != 0;
+      // a stand-in row adds exactly zero (its V is not a key of this row)
+      if (sizeof(T) == 2 && mb != nullptr && !keep[u]) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) vr[u][j] = u32x4{0u, 0u, 0u, 0u};
+      }
 #pragma unroll
       for (int g = 0; g < GC; ++g) {
         float t = 0.f;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) t = dot_chunk<T>(qr[g][j], kr[u][j], t);
         t = group_sum<LPR>(t) * a.scale_log2;
-        s[u][g] = keep ? t : -INFINITY;
+        s[u][g] = keep[u] ? t : -INFINITY;
       }
     }
 
@@ -289,12 +315,23 @@ __global__ __launch_bounds__(1024) void decode_split_kernel(DecodeArgs a) {
     }
   };
   const int grp = nw * RPW, step = U * grp;
-  int base = start;
-  for (; base + step <= end; base += step) pass(std::integral_constant<int, U>{}, base);
-  if (end - base > 2 * grp) {
-    pass(std::integral_constant<int, U>{}, base);
-  } else {
-    for (; base < end; base += grp) pass(std::integral_constant<int, 1>{}, base);
+  // the split in windows of kMaskWin rows with a mask (one window without)
+  const int win = mb != nullptr ? kMaskWin : (end > start ? end - start : 1);
+  for (wbase = start; wbase < end; wbase += win) {
+    wend = min(wbase + win, end);
+    if (mb != nullptr) {
+      __syncthreads();  // the previous window's mask reads are done
+      for (int i = tid; i < wend - wbase; i += blockDim.x)
+        msk[i] = mb[(int64_t)(wbase + i) * a.mask_sl] != 0;
+      __syncthreads();
+    }
+    int base = wbase;
+    for (; base + step <= wend; base += step) pass(std::integral_constant<int, U>{}, base);
+    if (wend - base > 2 * grp) {
+      pass(std::integral_constant<int, U>{}, base);
+    } else {
+      for (; base < wend; base += grp) pass(std::integral_constant<int, 1>{}, base);
+    }
   }
 
   // Merge the RPW row groups of this wave (butterfly over lane strides).
@@ -652,6 +689,7 @@ Plan make_plan(int32_t dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t L,
     nw = 8;
   // No more waves than the split has row-loads for.
   const HostGeom geo = host_geom(dtype, D);
+  if (dtype == MI_DTYPE_F32 && D >= 128 && nw > 8) nw = 8;   // split_max_threads
   while (nw > 1 && (int64_t)nw * geo.rpw * geo.u > p.split_len) nw >>= 1;
   p.nw = nw;
   return p;
@@ -663,7 +701,8 @@ hipError_t launch_split_t(const DecodeArgs& a, const Plan& p, int64_t B,
   dim3 grid((unsigned)a.num_splits, (unsigned)(Hkv * p.n_chunks),
             (unsigned)B);
   dim3 block((unsigned)(p.nw * 64));
-  const size_t shmem = (size_t)p.nw * GC * (D + 2) * sizeof(float);
+  size_t shmem = (size_t)p.nw * GC * (D + 2) * sizeof(float);
+  if (a.mask != nullptr) shmem += kMaskWin;
   hipLaunchKernelGGL((decode_split_kernel<T, D, GC>), grid, block, shmem,
                      stream, a);
   return hipGetLastError();

@@ -197,3 +197,29 @@ def test_split_pass_remainders(dev, D, base, rems):
         assert not torch.isnan(out).any(), (D, splits)
         assert max_abs(out, ref) < 2e-2, (D, splits)
         assert max_abs(lse, ref_lse) < LSE_TOL, (D, splits)
+
+
+@pytest.mark.parametrize("D,L,splits", [(128, 9000, 1), (128, 9000, 4), (64, 5000, 2), (64, 300, 3)])
+def test_mask_excluded_rows_are_not_read(dev, D, L, splits):
+    """The mask path streams only the rows the mask keeps: K/V rows it excludes
+    hold NaN and must not reach the output (the reference loads them and would
+    propagate the NaN through 0 * V).  L = 9000 with one split crosses the
+    4096-row mask windows; a window with every row excluded is included."""
+    B, Hq, Hkv = 3, 8, 2
+    q, k, v = _inputs(B, Hq, Hkv, L, D, torch.bfloat16, dev, seed=21)
+    g = torch.Generator().manual_seed(22)
+    mask = torch.rand((B, L), generator=g) < 0.5
+    mask[1, : min(L, 4500)] = False            # whole window(s) excluded
+    mask[2] = False
+    mask[2, L - 1] = True                      # a single key, the last one
+    kc, vc = k.clone(), v.clone()
+    keep = mask.to(dev)[:, None, :, None]
+    k = torch.where(keep, k, torch.full_like(k, float("nan")))
+    v = torch.where(keep, v, torch.full_like(v, float("nan")))
+    out, lse = _fd()(q, k, v, mask=mask.to(dev), num_splits=splits, return_lse=True)
+    assert not torch.isnan(out).any()
+    ref, ref_lse = ora.decode(q, kc, vc, mask=mask)
+    assert max_abs(out, ref) < 2e-2
+    empty = torch.isneginf(ref_lse)            # rows the mask empties entirely: -inf
+    assert torch.equal(torch.isneginf(lse.cpu()), empty)
+    assert max_abs(lse.cpu()[~empty], ref_lse[~empty]) < LSE_TOL
