@@ -65,10 +65,32 @@ __device__ inline bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
+// x from lane (lane ^ OFF) without LDS traffic: a DPP row rotate for 8, the
+// gfx950 permlane swap for 32.
+template <int OFF>
+__device__ inline float lm_lane_xor(float x, int lane) {
+  if constexpr (OFF == 8) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, true));
+  } else {
+    static_assert(OFF == 32, "lane stride");
+    auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                               false);
+    return __uint_as_float((lane & 32) ? sw[0] : sw[1]);
+  }
+}
+
 constexpr int kLmWaves = 4;
 constexpr int kLmBatch = 16;   // 16 MFMAs (512 k) per weight batch
 
-template <typename T>
+// DIAG (M <= 8): tiles of 8 weight rows, diagonal-packed -- A lanes of rows
+// r < 8 hold weight row r over the first 32 k of a 64-k step, rows r >= 8 the
+// same rows over the second 32 k; B columns c < 8 hold token row c over the
+// first half, c >= 8 token row c - 8 over the second; C[r][c] + C[r+8][c+8]
+// is the 64-k product.  A load instruction then reads 8 rows x 128 contiguous
+// bytes (whole cache lines) instead of 16 rows x 64 bytes, and no B column is
+// padding.  Otherwise (up to 16 rows): 16-row tiles, columns >= M zero.
+template <typename T, bool DIAG>
 __global__ __launch_bounds__(64 * kLmWaves) void lm_head_kernel(LmHeadArgs a) {
   using MM = HMfma<T>;
   typedef typename MM::v8 v8;
@@ -141,19 +163,24 @@ __global__ __launch_bounds__(64 * kLmWaves) void lm_head_kernel(LmHeadArgs a) {
   const int G = gridDim.x * kLmWaves;
   const int gw = blockIdx.x * kLmWaves + w;
   const int my_tiles = gw < a.n_tiles ? (a.n_tiles - 1 - gw) / G + 1 : 0;
-  const int KB = K / (32 * kLmBatch);           // weight batches per tile
+  constexpr int TR = DIAG ? 8 : 16;             // weight rows per tile
+  constexpr int KS = DIAG ? 64 : 32;            // k per MFMA
+  const int KB = K / (KS * kLmBatch);           // weight batches per tile
   const int n_steps = my_tiles * KB;
   const int r = lane & 15, g = lane >> 4;       // A: tile row / k group
+  const int rrow = DIAG ? (r & 7) : r;          // weight row within the tile
+  const int khalf = DIAG ? 32 * (r >> 3) : 0;   // k offset of this lane's half
   const int mcol = lane & 15;                   // B: x row (>= M: zero row)
-  const unsigned char* xb = xs + (mcol < M ? mcol : M) * row_b + g * 16;
+  const int xrow = DIAG ? (mcol & 7) : mcol;
+  const unsigned char* xb = xs + (xrow < M ? xrow : M) * row_b + g * 16 + khalf * 2;
   const T* wbase = reinterpret_cast<const T*>(a.w);
 
   auto issue = [&](u32x4 (&buf)[kLmBatch], int s) {
     const int t = gw + (s / KB) * G, kb = s % KB;
-    const int row = min(t * 16 + r, a.N - 1);   // rows past N: clamped, discarded
-    const T* p = wbase + (int64_t)row * a.w_sn + kb * 32 * kLmBatch + 8 * g;
+    const int row = min(t * TR + rrow, a.N - 1);  // rows past N: clamped, discarded
+    const T* p = wbase + (int64_t)row * a.w_sn + kb * KS * kLmBatch + khalf + 8 * g;
 #pragma unroll
-    for (int j = 0; j < kLmBatch; ++j) buf[j] = load16_stream(p + 32 * j);
+    for (int j = 0; j < kLmBatch; ++j) buf[j] = load16_stream(p + KS * j);
   };
   float best_v = -INFINITY;
   int best_i = 0x7fffffff;
@@ -163,16 +190,21 @@ __global__ __launch_bounds__(64 * kLmWaves) void lm_head_kernel(LmHeadArgs a) {
 #pragma unroll
     for (int j = 0; j < kLmBatch; ++j) {
       const v8 xv = __builtin_bit_cast(
-          v8, *reinterpret_cast<const u32x4*>(xb + (kb * 32 * kLmBatch + 32 * j) * 2));
+          v8, *reinterpret_cast<const u32x4*>(xb + (kb * KS * kLmBatch + KS * j) * 2));
       acc = MM::mma(__builtin_bit_cast(v8, buf[j]), xv, acc);
     }
     if (kb == KB - 1) {
-      // acc[i] = y[mcol][t*16 + 4g + i]
-      const int n0 = t * 16 + 4 * g;
+      if constexpr (DIAG) {
+        // fold the diagonal quadrants: lane + 40 holds C[4g + i + 8][c + 8]
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += lm_lane_xor<8>(lm_lane_xor<32>(acc[i], lane), lane);
+      }
+      // acc[i] = y[mcol][t*TR + 4g + i]  (DIAG: lanes g < 2, mcol < 8)
+      const int n0 = t * TR + 4 * g;
       T yv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) yv[i] = Elem<T>::from_f32(acc[i]);
-      if (mcol < M) {
+      if (mcol < M && (!DIAG || g < 2)) {
         T* yp = reinterpret_cast<T*>(a.y) + (int64_t)mcol * a.y_sm + n0;
         if (a.y_vec && n0 + 3 < a.N) {
           typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -280,12 +312,14 @@ __global__ __launch_bounds__(256) void lm_head_argmax_kernel(const float* part_v
 
 namespace {
 
-int lm_head_grid(int64_t n) {
+// Workgroups of a launch over `tiles` weight tiles (persistent: at most two per
+// CU); with 8-row tiles this also bounds the 16-row tiling's grid.
+int lm_head_grid_tiles(int64_t tiles) {
   const int cus = device_cu_count();
-  const int64_t tiles = (n + 15) / 16;
   const int64_t groups = (tiles + kLmWaves - 1) / kLmWaves;
   return (int)(groups < 2 * cus ? groups : 2 * cus);
 }
+int lm_head_grid(int64_t n) { return lm_head_grid_tiles((n + 7) / 8); }
 
 }  // namespace
 }  // namespace mi
@@ -325,7 +359,9 @@ extern "C" int32_t mi_lm_head(const void* x, int64_t x_sm, const void* norm_w, f
     set_last_error("lm_head: x / w / norm_w rows must be 16-byte aligned");
     return MI_ERR_INVALID;
   }
-  const int grid = lm_head_grid(n);
+  // diagonal-packed 8-row tiles for up to 8 rows (64-k MFMA steps, 1024-k batches)
+  const bool diag = m <= 8 && k % (64 * kLmBatch) == 0;
+  const int grid = lm_head_grid_tiles(diag ? (n + 7) / 8 : (n + 15) / 16);
   if (argmax_out != nullptr && (part_v == nullptr || part_i == nullptr || n_parts < grid)) {
     set_last_error("lm_head: argmax needs partial buffers of >= %d entries per row", grid);
     return MI_ERR_INVALID;
@@ -336,15 +372,22 @@ extern "C" int32_t mi_lm_head(const void* x, int64_t x_sm, const void* norm_w, f
   a.part_i = argmax_out != nullptr ? part_i : nullptr;
   a.x_sm = x_sm; a.w_sn = w_sn; a.y_sm = y_sm;
   a.M = (int32_t)m; a.K = (int32_t)k; a.N = (int32_t)n;
-  a.n_tiles = (int32_t)((n + 15) / 16);
+  a.n_tiles = (int32_t)(diag ? (n + 7) / 8 : (n + 15) / 16);
   a.n_parts = (int32_t)(argmax_out != nullptr ? n_parts : 0);
   a.y_vec = (py % 8 == 0 && (y_sm * 2) % 8 == 0) ? 1 : 0;
   const size_t shmem = (size_t)(m + 1) * (size_t)(k * 2 + 16);
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == MI_DTYPE_BF16)
-    hipLaunchKernelGGL(lm_head_kernel<bf16_t>, dim3(grid), dim3(64 * kLmWaves), shmem, st, a);
-  else
-    hipLaunchKernelGGL(lm_head_kernel<f16_t>, dim3(grid), dim3(64 * kLmWaves), shmem, st, a);
+  if (dtype == MI_DTYPE_BF16) {
+    if (diag)
+      hipLaunchKernelGGL((lm_head_kernel<bf16_t, true>), dim3(grid), dim3(64 * kLmWaves), shmem, st, a);
+    else
+      hipLaunchKernelGGL((lm_head_kernel<bf16_t, false>), dim3(grid), dim3(64 * kLmWaves), shmem, st, a);
+  } else {
+    if (diag)
+      hipLaunchKernelGGL((lm_head_kernel<f16_t, true>), dim3(grid), dim3(64 * kLmWaves), shmem, st, a);
+    else
+      hipLaunchKernelGGL((lm_head_kernel<f16_t, false>), dim3(grid), dim3(64 * kLmWaves), shmem, st, a);
+  }
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && argmax_out != nullptr) {
     hipLaunchKernelGGL(lm_head_argmax_kernel, dim3((unsigned)m), dim3(256), 0, st, part_v, part_i,
