@@ -441,7 +441,10 @@ __global__ __launch_bounds__(64 * NW) void dgemv_kernel(LayerGemvArgs a) {
   const int rr = r16 & 7;                // A: tile row / B: token row
   const int kofs = (r16 >> 3) * 64 + 16 * g;
   const bool m_ok = rr < a.M;
-  const int kw = w * SC * 128;
+  // K slice of this wave, rotated by block so that concurrent blocks do not all
+  // read the same x lines at the same time
+  const int ks = (w + (int)blockIdx.x) % NW;
+  const int kw = ks * SC * 128;
 
   // ---- which matrix / tiles this block owns
   int mat0 = 0, tile0 = blockIdx.x * TPB;
