@@ -138,6 +138,19 @@ int32_t mi_flash_decode_noalloc(const void* q, const void* k, const void* v,
                                 void* stream);
 
 /*
+ * Split count flash_decode runs for a requested num_splits on the current
+ * device: unchanged once B * kv-head-groups * num_splits blocks cover the
+ * compute units; below that, each requested split is subdivided into key
+ * ranges of >= 1024 keys until they do (the output differs from the requested
+ * split only in fp32 summation order).  The Python flash_decode and
+ * mi_flash_decode_noalloc apply it; mi_flash_decode / mi_decode_split run
+ * exactly the num_splits they are given.  No counterpart in the reference
+ * (whose split size is fixed at 256 keys, src/flash_decode.py:271-272).
+ */
+int64_t mi_decode_effective_splits(int64_t batch, int64_t n_heads, int64_t n_kv_heads,
+                                   int64_t kv_len, int64_t head_dim, int64_t num_splits);
+
+/*
  * Split count the library would pick for a decode of this shape on the
  * current device (used when the caller passes no explicit num_splits).
  */

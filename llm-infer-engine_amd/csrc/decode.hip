@@ -922,6 +922,27 @@ extern "C" int64_t mi_decode_default_splits(int64_t batch, int64_t n_heads,
   return s;
 }
 
+extern "C" int64_t mi_decode_effective_splits(int64_t batch, int64_t n_heads,
+                                              int64_t n_kv_heads, int64_t kv_len,
+                                              int64_t head_dim, int64_t num_splits) {
+  if (batch <= 0 || n_heads <= 0 || n_kv_heads <= 0 || kv_len <= 0 || num_splits <= 1)
+    return num_splits < 1 ? 1 : num_splits;
+  const int64_t G = n_heads / n_kv_heads;
+  const int gmax = gc_max(MI_DTYPE_BF16, head_dim > 0 ? head_dim : 128);
+  const int64_t units = batch * n_kv_heads * ((G + gmax - 1) / gmax);
+  const int64_t cus = device_cu_count();
+  if (units * num_splits >= cus) return num_splits;
+  // each requested split becomes f key ranges until the blocks cover the CUs,
+  // keeping >= 1024 keys a range (short calls keep their split count)
+  int64_t f = (cus + units * num_splits - 1) / (units * num_splits);
+  const int64_t f_keys = kv_len / (1024 * num_splits);
+  if (f > f_keys) f = f_keys;
+  if (f < 1) f = 1;
+  int64_t s = num_splits * f;
+  if (s > kMaxSplits) s = num_splits;
+  return s;
+}
+
 extern "C" int32_t mi_decode_split(
     const void* q, const void* k, const void* v, const uint8_t* mask,
     int64_t mask_sb, int64_t mask_sl, const int64_t* seq_lens, float* part_m,
@@ -1074,6 +1095,9 @@ extern "C" int32_t mi_flash_decode_noalloc(
                            nullptr, out, lse, batch, n_heads, n_kv_heads, kv_len, head_dim,
                            1, q_sb, q_sh, q_sd, k_sb, k_sh, k_sl, v_sb, v_sh, v_sl, o_sb,
                            o_sh, o_sd, sm_scale, empty_rows_nan, dtype, stream);
+  // fewer splits than fill the GPU are subdivided, as flash_decode does
+  num_splits = mi_decode_effective_splits(batch, n_heads, n_kv_heads, kv_len, head_dim,
+                                          num_splits);
   // layout in scratch: acc [B*Hq*S*D] fp32, then m and l [B*Hq*S] fp32 each,
   // every array starting on a 256-byte boundary
   const int64_t rows = batch * n_heads * num_splits;

@@ -81,6 +81,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _f32, _i32, _i32, _ptr,                # sm_scale empty_nan dtype stream
     ]),
     "mi_decode_default_splits": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "mi_decode_effective_splits": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "mi_attn_prefill": (_i32, [
         _ptr, _ptr, _ptr, _ptr, _ptr,          # q k v out lse
         _i64, _i64, _i64, _i64, _i64, _i64,    # B Hq Hkv S L D

@@ -76,6 +76,9 @@ def _run_decode(q, k, v, mask, seq_lens, num_splits, return_lse, empty_nan, what
     if num_splits < 1:
         raise ValueError(f"num_splits must be >= 1, got {num_splits}")
     num_splits = min(num_splits, kv_len)
+    # too few splits to fill the GPU are subdivided into >= 1024-key ranges
+    num_splits = int(_lib.load().mi_decode_effective_splits(
+        batch_size, n_heads, n_kv_heads, kv_len, head_dim, num_splits))
     k = _kv_ready(k)
     v = _kv_ready(v)
     out = torch.empty_like(q)
