@@ -140,13 +140,19 @@ struct DecodeGeom {
 // windows of this many rows).
 constexpr int kMaskWin = 4096;
 
-// fp32 K/V at head_dim >= 128 hold twice the registers per row chunk: those
-// kernels run at most 8 waves (512 threads, 256 VGPRs), the others up to 16.
-template <typename T, int D>
-constexpr int split_max_threads() { return (sizeof(T) == 4 && D >= 128) ? 512 : 1024; }
+// fp32 K/V at head_dim >= 128 hold twice the registers per row chunk, and the
+// masked 2-byte kernels with 4 heads per block add the row selection to the
+// largest score tile: those kernels run at most 8 waves (512 threads, 256
+// VGPRs), the others up to 16 (128 VGPRs).
+template <typename T, int D, int GC, bool MASK>
+constexpr int split_max_threads() {
+  return ((sizeof(T) == 4 && D >= 128) || (sizeof(T) == 2 && MASK && GC >= 4)) ? 512 : 1024;
+}
 
-template <typename T, int D, int GC>
-__global__ __launch_bounds__((split_max_threads<T, D>())) void decode_split_kernel(DecodeArgs a) {
+// MASK: a.mask is set (rows are staged per window and the mask-excluded ones
+// are not streamed); the no-mask instantiation is a single window.
+template <typename T, int D, int GC, bool MASK>
+__global__ __launch_bounds__((split_max_threads<T, D, GC, MASK>())) void decode_split_kernel(DecodeArgs a) {
   using Geo = DecodeGeom<T, D>;
   constexpr int EPC = Geo::kEPC, LPR = Geo::kLPR, CPL = Geo::kCPL,
                 E = Geo::kE, RPW = Geo::kRPW, U = Geo::kU;
@@ -220,21 +226,20 @@ __global__ __launch_bounds__((split_max_threads<T, D>())) void decode_split_kern
                 (int64_t)kvh * a.k_sh + li * EPC;
   const T* vb = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb +
                 (int64_t)kvh * a.v_sh + li * EPC;
-  const uint8_t* mb =
-      a.mask != nullptr ? a.mask + (int64_t)b * a.mask_sb : nullptr;
+  const uint8_t* mb = MASK ? a.mask + (int64_t)b * a.mask_sb : nullptr;
   const int my_off = w * RPW + rg;
   // With a mask, the bytes of the current window of rows are staged in LDS
   // (after the wave-merge area) so a pass knows which rows to fetch before it
   // issues their loads: excluded rows are not streamed.
   unsigned char* msk = reinterpret_cast<unsigned char*>(smem + nw * GC * (D + 2));
-  int wbase = start, wend = end;
 
   // One pass over UU row groups per wave (UU * nw * RPW keys from `base`).
   // Full passes of U groups cover the split; a remainder of at most two
   // groups runs in one-group passes (so a split just past a multiple of the
   // U-group step does not pay a whole U-group pass for a few keys), a longer
   // one in one more U-group pass (one round trip instead of up to U).
-  auto pass = [&](auto uu_c, const int base) __attribute__((always_inline)) {
+  auto pass = [&](auto uu_c, const int base, const int wbase, const int wend)
+      __attribute__((always_inline)) {
     constexpr int UU = decltype(uu_c)::value;
     u32x4 kr[UU][CPL], vr[UU][CPL];
     int row[UU];
@@ -242,34 +247,40 @@ __global__ __launch_bounds__((split_max_threads<T, D>())) void decode_split_kern
     for (int u = 0; u < UU; ++u) {
       row[u] = base + u * nw * RPW + my_off;
     }
-    // Rows past the window, and rows the mask excludes, re-read the window's
-    // last row (always in bounds, never a key beyond seq_lens: a cache hit,
-    // not a stream) and are dropped from the softmax below.
-    bool keep[UU];
-    int rl[UU];
+    // Rows past the window re-read the window's last row (always in bounds,
+    // never a key beyond seq_lens: a cache hit, not a stream) and are dropped
+    // from the softmax below; with a mask, so are the rows it excludes (2-byte
+    // K/V; fp32 keeps the plain clamp, the 1024-thread kernels have no
+    // registers to spare for the row selection).
+    auto src_row = [&](const int r) __attribute__((always_inline)) -> int64_t {
+      int x = min(r, wend - 1);
+      if constexpr (sizeof(T) == 2 && MASK) {
+        if (r < wend && msk[r - wbase] == 0) x = wend - 1;
+      }
+      return x;
+    };
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
-      keep[u] = row[u] < wend;
-      if (mb != nullptr && keep[u]) keep[u] = msk[row[u] - wbase] != 0;
-      // (fp32 K/V keep the plain clamp: the 1024-thread kernels have no
-      // registers to spare for the row selection)
-      rl[u] = sizeof(T) == 2 ? (keep[u] ? row[u] : wend - 1) : min(row[u], wend - 1);
+      const int64_t rl = src_row(row[u]);
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
-        kr[u][j] = load16_stream(kb + (int64_t)rl[u] * a.k_sl + j * LPR * EPC);
+        kr[u][j] = load16_stream(kb + rl * a.k_sl + j * LPR * EPC);
     }
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
+      const int64_t rl = src_row(row[u]);
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
-        vr[u][j] = load16_stream(vb + (int64_t)rl[u] * a.v_sl + j * LPR * EPC);
+        vr[u][j] = load16_stream(vb + rl * a.v_sl + j * LPR * EPC);
     }
 
     float s[UU][GC];
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
+      bool keep = row[u] < wend;
+      if (MASK && keep) keep = msk[row[u] - wbase] != 0;
       // a stand-in row adds exactly zero (its V is not a key of this row)
-      if (sizeof(T) == 2 && mb != nullptr && !keep[u]) {
+      if (sizeof(T) == 2 && MASK && !keep) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) vr[u][j] = u32x4{0u, 0u, 0u, 0u};
       }
@@ -279,7 +290,7 @@ __global__ __launch_bounds__((split_max_threads<T, D>())) void decode_split_kern
 #pragma unroll
         for (int j = 0; j < CPL; ++j) t = dot_chunk<T>(qr[g][j], kr[u][j], t);
         t = group_sum<LPR>(t) * a.scale_log2;
-        s[u][g] = keep[u] ? t : -INFINITY;
+        s[u][g] = keep ? t : -INFINITY;
       }
     }
 
@@ -316,22 +327,27 @@ __global__ __launch_bounds__((split_max_threads<T, D>())) void decode_split_kern
   };
   const int grp = nw * RPW, step = U * grp;
   // the split in windows of kMaskWin rows with a mask (one window without)
-  const int win = mb != nullptr ? kMaskWin : (end > start ? end - start : 1);
-  for (wbase = start; wbase < end; wbase += win) {
-    wend = min(wbase + win, end);
-    if (mb != nullptr) {
+  auto run_window = [&](const int wbase, const int wend) __attribute__((always_inline)) {
+    int base = wbase;
+    for (; base + step <= wend; base += step)
+      pass(std::integral_constant<int, U>{}, base, wbase, wend);
+    if (wend - base > 2 * grp) {
+      pass(std::integral_constant<int, U>{}, base, wbase, wend);
+    } else {
+      for (; base < wend; base += grp) pass(std::integral_constant<int, 1>{}, base, wbase, wend);
+    }
+  };
+  if constexpr (MASK) {
+    for (int wbase = start; wbase < end; wbase += kMaskWin) {
+      const int wend = min(wbase + kMaskWin, end);
       __syncthreads();  // the previous window's mask reads are done
       for (int i = tid; i < wend - wbase; i += blockDim.x)
         msk[i] = mb[(int64_t)(wbase + i) * a.mask_sl] != 0;
       __syncthreads();
+      run_window(wbase, wend);
     }
-    int base = wbase;
-    for (; base + step <= wend; base += step) pass(std::integral_constant<int, U>{}, base);
-    if (wend - base > 2 * grp) {
-      pass(std::integral_constant<int, U>{}, base);
-    } else {
-      for (; base < wend; base += grp) pass(std::integral_constant<int, 1>{}, base);
-    }
+  } else {
+    run_window(start, end);
   }
 
   // Merge the RPW row groups of this wave (butterfly over lane strides).
@@ -700,11 +716,17 @@ hipError_t launch_split_t(const DecodeArgs& a, const Plan& p, int64_t B,
                           int64_t Hkv, hipStream_t stream) {
   dim3 grid((unsigned)a.num_splits, (unsigned)(Hkv * p.n_chunks),
             (unsigned)B);
-  dim3 block((unsigned)(p.nw * 64));
-  size_t shmem = (size_t)p.nw * GC * (D + 2) * sizeof(float);
-  if (a.mask != nullptr) shmem += kMaskWin;
-  hipLaunchKernelGGL((decode_split_kernel<T, D, GC>), grid, block, shmem,
-                     stream, a);
+  if (a.mask != nullptr) {
+    const int nw = min(p.nw, split_max_threads<T, D, GC, true>() / 64);
+    const size_t shmem = (size_t)nw * GC * (D + 2) * sizeof(float) + kMaskWin;
+    hipLaunchKernelGGL((decode_split_kernel<T, D, GC, true>), grid, dim3((unsigned)(nw * 64)),
+                       shmem, stream, a);
+  } else {
+    const int nw = min(p.nw, split_max_threads<T, D, GC, false>() / 64);
+    const size_t shmem = (size_t)nw * GC * (D + 2) * sizeof(float);
+    hipLaunchKernelGGL((decode_split_kernel<T, D, GC, false>), grid, dim3((unsigned)(nw * 64)),
+                       shmem, stream, a);
+  }
   return hipGetLastError();
 }
 
