@@ -104,6 +104,8 @@ __device__ inline int v_swz(int r) { return (r >> 1) & 3; }  // XOR mask for V r
 // probabilities stay <= 2^8 (exact maths is unchanged: O and l share the same
 // reference max) and O is rescaled on rare tiles instead of on every tile.
 constexpr float kRescaleThreshold = 8.0f;
+// Row-sum bound of the max-free softmax half (16 scores per lane): 16 * 2^8.
+constexpr float kFastSumLimit = 4096.0f;
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
@@ -644,6 +646,57 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
     }
     return resc;
   };
+  // Softmax of one half against the running max, without the half's own max:
+  // every p is at most the lane's row sum of the half, so while that sum stays
+  // at or below 16 * 2^kRescaleThreshold no p exceeds 2^(kRescaleThreshold + 4)
+  // and the running max may stay (the same lazy rule as above, with 4 more
+  // bits of headroom).  Returns true (uniform over the wave) when some lane's
+  // sum is larger; the caller then runs smax on the same scores, which finds
+  // the max, moves it and recomputes P (the scores are left intact here apart
+  // from the causal mask).  A wave's first tile always takes that path (its
+  // running max is still kNegBig).
+  auto smax_fast = [&](f32x16 (&s)[2], v8 (&p)[2][2], auto use0_c, auto mask0_c, auto mask1_c) {
+    constexpr bool USE0 = decltype(use0_c)::value;
+    constexpr bool MASK[2] = {decltype(mask0_c)::value, decltype(mask1_c)::value};
+    float lsum[2] = {0.f, 0.f};
+    bool big = false;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      if (rb == 0 && !USE0) continue;
+      if (MASK[rb]) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (16 * (i >> 3) + (i & 7) > tri) s[rb][i] = -INFINITY;
+      }
+      const float mr = m[rb];
+      float ls0 = 0.f, ls1 = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        uint32_t wd[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float e0 = fast_exp2(fmaf(s[rb][8 * cc + 2 * t], sl2, -mr));
+          const float e1 = fast_exp2(fmaf(s[rb][8 * cc + 2 * t + 1], sl2, -mr));
+          if (t & 1) ls1 += e0 + e1; else ls0 += e0 + e1;
+          wd[t] = MM::pack2(e0, e1);
+        }
+        p[rb][cc] = __builtin_bit_cast(v8, u32x4{wd[0], wd[1], wd[2], wd[3]});
+      }
+      lsum[rb] = ls0 + ls1;
+      big = big || !(lsum[rb] <= kFastSumLimit);
+    }
+    const bool fb = __builtin_amdgcn_ballot_w64(big) != 0;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      if (rb == 0 && !USE0) continue;
+      l[rb] = fb ? l[rb] : l[rb] + lsum[rb];
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+        __asm__ volatile("" ::"v"(__builtin_bit_cast(u32x4, p[rb][cc])));
+      __asm__ volatile("" ::"v"(l[rb]));
+    }
+    return fb;
+  };
   auto rescale_o = [&](auto use0_c) {
     constexpr bool USE0 = decltype(use0_c)::value;
 #pragma unroll
@@ -674,7 +727,7 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x402, 9, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x402, 7, 0);  // VALU
     }
   };
   // slot A(t): softmax(t.h0) | PV(t-1.h1), QK(t.h1).  HAS_PV: t > 0;
@@ -683,9 +736,15 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
     constexpr bool HAS_PV = decltype(has_pv_c)::value, DIAG = decltype(diag_c)::value;
     if constexpr (HAS_PV) pv(prv, 1, pB, TT{});
     qk(cur, 1, sB, std::integral_constant<bool, !DIAG>{});
-    const bool resc = smax(sA, pA, TT{}, std::integral_constant<bool, DIAG>{}, FF{});
-    if constexpr (HAS_PV && !DIAG) interleave();
-    if (resc) rescale_o(TT{});
+    if constexpr (!HAS_PV) {  // the wave's first tile: no running max yet
+      if (smax(sA, pA, TT{}, std::integral_constant<bool, DIAG>{}, FF{})) rescale_o(TT{});
+    } else {
+      const bool fb = smax_fast(sA, pA, TT{}, std::integral_constant<bool, DIAG>{}, FF{});
+      if constexpr (!DIAG) interleave();
+      if (fb) {
+        if (smax(sA, pA, TT{}, std::integral_constant<bool, DIAG>{}, FF{})) rescale_o(TT{});
+      }
+    }
   };
   // slot B(t): softmax(t.h1) | PV(t.h0), QK(t+1.h0); on the diagonal tile,
   // rb 1 only, followed by the drain PV(t.h1).
@@ -694,11 +753,15 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
     pv(cur, 0, pA, TT{});
     if constexpr (!DIAG) {
       qk(nxt, 0, sA, TT{});
-      const bool resc = smax(sB, pB, TT{}, FF{}, FF{});
+      const bool fb = smax_fast(sB, pB, TT{}, FF{}, FF{});
       interleave();
-      if (resc) rescale_o(TT{});
+      if (fb) {
+        if (smax(sB, pB, TT{}, FF{}, FF{})) rescale_o(TT{});
+      }
     } else {
-      if (smax(sB, pB, FF{}, FF{}, TT{})) rescale_o(FF{});
+      if (smax_fast(sB, pB, FF{}, FF{}, TT{})) {
+        if (smax(sB, pB, FF{}, FF{}, TT{})) rescale_o(FF{});
+      }
       pv(cur, 1, pB, FF{});
     }
   };
