@@ -6,8 +6,10 @@ Headline (`value`): BASELINE config 2 — causal GQA prefill, bf16, B4 S2048
 `extra`, the HBM-bound decode configs (3: B16 24/8 D128 T8192 ragged lengths;
 4: B1 L=131072, split sweep) in GB/s, the W8A16 decode step (config 5) in
 tokens/s, and the W8A16 prefill GEMM (one layer's projections at config 2's
-8192 tokens) in TFLOP/s, each with its own roofline; and the CPU baseline (the
-fp32 oracle on the host cores, one bounded sample per config, under each leg).
+8192 tokens) in TFLOP/s, each with its own roofline; config 1 and config 2's
+attention block in the model layout (RoPE(K) + KV append + attention with q's
+RoPE fused) in TFLOP/s; and the CPU baseline (the fp32 oracle on the host
+cores, one bounded sample per config, under each leg).
 
 A step is one flash_attention call on resident inputs.  Timing: untimed
 warm-up (at least W steps and at least 0.25 s of back-to-back steps, so the GPU
@@ -516,6 +518,61 @@ def bench_prefill_cfg1(torch, steps: int, warmup: int) -> dict:
             "ms_per_step": ms, "flops": flops}
 
 
+def bench_prefill_model_layout(torch, steps: int, warmup: int) -> dict:
+    """Config 2's attention block as the model runs it (src/model.py Attention,
+    the reference's src/model.py:57-79): q/k/v are views of [B, S, H, D]
+    projection outputs, RoPE(K) + V are appended to a KV cache of capacity
+    4096, and attention reads q (RoPE'd in the kernel's Q prologue) against the
+    cache views.  Also timed: the same with RoPE(q) as its own launch
+    (apply_rotary, the reference's sequence)."""
+    from src.config import ModelArgs
+    from src.flash_attn import flash_attention
+    from src.kv_cache import KVCache
+    from src.rope import DeviceRopeTable, apply_rotary, precompute_freqs_cis, rope_and_cache_update
+    dev = torch.device("cuda:0")
+    B, S, Hq, Hkv, D, T = 4, 2048, 32, 8, 64, 4096
+    args = ModelArgs(dim=Hq * D, n_layers=1, n_heads=Hq, n_kv_heads=Hkv, max_batch_size=B,
+                     max_seq_len=T, device=str(dev))
+    kv = KVCache(args, dtype=torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def proj(h):
+        return torch.randn((B, S, h * D), device=dev, generator=g).to(torch.bfloat16) \
+            .view(B, S, h, D).transpose(1, 2)
+    xq, xk, xv = proj(Hq), proj(Hkv), proj(Hkv)
+    cos, sin = DeviceRopeTable(precompute_freqs_cis(D, T), torch.bfloat16, dev).rows(0, S)
+    flops = 4.0 * B * Hq * S * S * D / 2
+
+    def fused(i):
+        ck, cv = rope_and_cache_update(xk, xv, cos, sin, kv, 0, start_pos=0)
+        return flash_attention(xq, ck, cv, rope_cos=cos, rope_sin=sin)
+
+    def separate(i):
+        q = apply_rotary(xq, cos, sin)
+        ck, cv = rope_and_cache_update(xk, xv, cos, sin, kv, 0, start_pos=0)
+        return flash_attention(q, ck, cv)
+
+    def append_only(i):
+        return rope_and_cache_update(xk, xv, cos, sin, kv, 0, start_pos=0)
+    res = {}
+    # several calls per graph, so the host's replay submission is not what is timed
+    for name, fn, n in (("fused", fused, 4), ("separate_q_rope", separate, 4),
+                        ("rope_k_append", append_only, 16)):
+        graph = _graph_decode(torch, fn, n)
+        res[name] = _time_graph(torch, graph, n, max(steps, 4 * n), warmup)
+        del graph
+    ms = res["fused"]
+    kbytes = B * Hkv * S * D * 2 * 4  # K and V read, RoPE(K) and V written
+    return {"config": "2 in the model layout: RoPE(K) + KV append (T 4096) + attention with "
+                      "RoPE(q) in the kernel, q/k/v views of [B,S,H,D] projections",
+            "value": round(flops / (ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s", "ms_per_step": ms,
+            "flops": flops,
+            "separate_q_rope": {"ms_per_step": res["separate_q_rope"],
+                                "value": round(flops / (res["separate_q_rope"] * 1e-3) / 1e12, 1)},
+            "rope_k_append": {"ms": res["rope_k_append"], "bytes": kbytes,
+                              "GB/s": round(kbytes / (res["rope_k_append"] * 1e-3) / 1e9, 1)}}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -550,6 +607,8 @@ def main() -> None:
     if args.only in (None, "prefill"):
         pre = bench_prefill(torch, args.steps, args.warmup)
         extra["prefill_config1"] = bench_prefill_cfg1(torch, args.steps, args.warmup)
+        extra["prefill_config2_model_layout"] = bench_prefill_model_layout(torch, args.steps,
+                                                                           args.warmup)
     if args.only in (None, "decode"):
         extra["decode_config3"] = bench_decode_cfg3(torch, args.steps, args.warmup)
         extra["decode_config4"] = bench_decode_cfg4(torch, args.steps, args.warmup)

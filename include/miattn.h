@@ -219,6 +219,28 @@ int32_t mi_attn_prefill(const void* q, const void* k, const void* v, void* out,
                         int32_t dtype, void* stream);
 
 /*
+ * mi_attn_prefill with the rotate-half RoPE of q applied in the kernel's Q
+ * prologue (q is read unrotated and never written): query row s of every
+ * head uses row positions[s] of cos/sin (clamped into [0, table_rows)), or
+ * row s when positions is NULL.  cos/sin [table_rows, >= head_dim/2] in q's
+ * dtype, unit column stride, 16-byte aligned rows of table_row_stride
+ * elements.  bf16/fp16 only (fp32: mi_rope, then mi_attn_prefill).  The
+ * result is bitwise that of mi_rope on q followed by mi_attn_prefill.
+ * Replaces apply_rotary(xq) + flash_attention of one prefill step
+ *   src/rope.py:48-119 (rope_kernel, apply_rotary), src/flash_attn.py:5-111,
+ *   as called by src/model.py:62-79.
+ */
+int32_t mi_attn_prefill_rope(const void* q, const void* k, const void* v, void* out,
+                             float* lse, int64_t batch, int64_t n_heads, int64_t n_kv_heads,
+                             int64_t seq_len, int64_t kv_len, int64_t head_dim, int64_t q_sb,
+                             int64_t q_sh, int64_t q_ss, int64_t k_sb, int64_t k_sh,
+                             int64_t k_ss, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                             int64_t o_sb, int64_t o_sh, int64_t o_ss, float sm_scale,
+                             const void* cos, const void* sin, int64_t table_rows,
+                             int64_t table_row_stride, const int64_t* positions,
+                             int32_t dtype, void* stream);
+
+/*
  * RMSNorm over the last dim: y[r] = x[r] * rsqrt(mean(x[r]^2) + eps) * w,
  * fp32 internally, y in x's dtype (wdtype = weight dtype).  rows x n with row
  * strides x_rs / y_rs.

@@ -167,6 +167,22 @@ __device__ inline uint32_t lds_addr(const unsigned char* p) {
 }
 __device__ inline void dma_wait_all() { __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// One rotate-half RoPE pair (x1 = x[i], x2 = x[i + D/2], c/s = cos/sin[i]):
+// y1 = x1*c - x2*s, y2 = x2*c + x1*s in fp32 with no contraction -- products
+// and the sum each rounded to fp32 (an fma, or a fused fma_mix f16
+// conversion, would round once and can differ in the last bit) -- then
+// rounded once to T.  Shared by the RoPE kernels and the prefill kernels'
+// Q prologue, so both give the same bits.
+template <typename T, typename CT>
+__device__ inline void rope_rotate(float x1, float x2, CT cv, CT sv, T& y1, T& y2) {
+#pragma clang fp contract(off)
+  const float c = Elem<CT>::to_f32(cv), s = Elem<CT>::to_f32(sv);
+  const float x1c = x1 * c, x2s = x2 * s, x2c = x2 * c, x1s = x1 * s;
+  const float r1 = x1c - x2s, r2 = x2c + x1s;
+  y1 = Elem<T>::from_f32(r1);
+  y2 = Elem<T>::from_f32(r2);
+}
+
 __device__ inline void block_sync_lds() {
   // LDS reads of this wave are complete and every wave has arrived; the
   // tile copies (vmcnt) are waited for separately where a tile is published.

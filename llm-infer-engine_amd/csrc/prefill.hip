@@ -55,7 +55,42 @@ struct PrefillArgs {
   int32_t pj;               // 32-row slices per head per block
   int32_t n_pb;             // position blocks (of 32*pj rows)
   float scale_log2;         // sm_scale * log2(e)
+  // Optional RoPE of q in the Q prologue (rcos == nullptr: q is used as
+  // given).  Rotate-half with the table row rpos[s] (or s when rpos is null)
+  // of cos/sin [rows, D/2] in q's dtype, unit column stride, row stride r_ss.
+  const void* rcos;
+  const void* rsin;
+  const int64_t* rpos;
+  int64_t r_ss, r_rows;     // positions are clamped into the table's rows
 };
+
+// RoPE of the Q fragments a lane holds for one 32-row block: chunk c (dims
+// 16c + 8hh .. +7) pairs with chunk c + DC/2 (the same dims + D/2), so every
+// rotation pair is in the lane's own registers.  qrow is the lane's query row
+// (clamped into [0, S)); the rounding is that of the RoPE kernels.
+template <typename T, int DC, typename V8>
+__device__ inline void rope_q_fragments(const PrefillArgs& a, int qrow, int hh, V8 (&qf)[DC]) {
+  int64_t crow = qrow;
+  if (a.rpos != nullptr) crow = min(max(a.rpos[qrow], (int64_t)0), a.r_rows - 1);
+  const T* cp = reinterpret_cast<const T*>(a.rcos) + crow * a.r_ss;
+  const T* sp = reinterpret_cast<const T*>(a.rsin) + crow * a.r_ss;
+#pragma unroll
+  for (int c = 0; c < DC / 2; ++c) {
+    const int i0 = 16 * c + 8 * hh;
+    const V8 cv = __builtin_bit_cast(V8, load16(cp + i0));
+    const V8 sv = __builtin_bit_cast(V8, load16(sp + i0));
+    V8 lo = qf[c], hi = qf[c + DC / 2];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      T y1, y2;
+      rope_rotate<T, T>(Elem<T>::to_f32(lo[e]), Elem<T>::to_f32(hi[e]), cv[e], sv[e], y1, y2);
+      lo[e] = y1;
+      hi[e] = y2;
+    }
+    qf[c] = lo;
+    qf[c + DC / 2] = hi;
+  }
+}
 
 template <typename T> struct Mfma;
 template <> struct Mfma<bf16_t> {
@@ -181,6 +216,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
       if (qrow >= a.S) raw = u32x4{0, 0, 0, 0};
       qreg[rb][c] = __builtin_bit_cast(v8, raw);
     }
+    if (a.rcos != nullptr) rope_q_fragments<T, DC>(a, min(qrow, a.S - 1), hh, qreg[rb]);
   }
 
   // ---- DMA geometry: wave w copies 1 KB pieces (w*NI + i) of each tile
@@ -497,6 +533,7 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
       if (qrow >= a.S) raw = u32x4{0, 0, 0, 0};
       qreg[rb][c] = __builtin_bit_cast(v8, raw);
     }
+    if (a.rcos != nullptr) rope_q_fragments<T, DC>(a, min(qrow, a.S - 1), hh, qreg[rb]);
   }
 
   // ---- tile copies: wave w copies 1 KB pieces (w*NI + i) of each tile
@@ -919,16 +956,22 @@ hipError_t launch_sp(const PrefillArgs& a, hipStream_t stream) {
 
 using namespace mi;
 
-extern "C" int32_t mi_attn_prefill(const void* q, const void* k, const void* v,
-                                   void* o, float* lse, int64_t batch,
-                                   int64_t n_heads, int64_t n_kv_heads,
-                                   int64_t seq_len, int64_t kv_len,
-                                   int64_t head_dim, int64_t q_sb, int64_t q_sh,
-                                   int64_t q_ss, int64_t k_sb, int64_t k_sh,
-                                   int64_t k_ss, int64_t v_sb, int64_t v_sh,
-                                   int64_t v_ss, int64_t o_sb, int64_t o_sh,
-                                   int64_t o_ss, float sm_scale, int32_t dtype,
-                                   void* stream) {
+namespace {
+
+// Q RoPE for the prologue (cos == nullptr: none).
+struct RopeQ {
+  const void* cos = nullptr;
+  const void* sin = nullptr;
+  const int64_t* pos = nullptr;
+  int64_t row_stride = 0, rows = 0;
+};
+
+int32_t attn_prefill(const void* q, const void* k, const void* v, void* o, float* lse,
+                     int64_t batch, int64_t n_heads, int64_t n_kv_heads, int64_t seq_len,
+                     int64_t kv_len, int64_t head_dim, int64_t q_sb, int64_t q_sh,
+                     int64_t q_ss, int64_t k_sb, int64_t k_sh, int64_t k_ss, int64_t v_sb,
+                     int64_t v_sh, int64_t v_ss, int64_t o_sb, int64_t o_sh, int64_t o_ss,
+                     float sm_scale, int32_t dtype, const RopeQ& rq, void* stream) {
   if (q == nullptr || k == nullptr || v == nullptr || o == nullptr) {
     set_last_error("attn_prefill: null pointer");
     return MI_ERR_INVALID;
@@ -997,6 +1040,8 @@ extern "C" int32_t mi_attn_prefill(const void* q, const void* k, const void* v,
   const int rows_per_block = sp ? 64 * pj : 32 * prefill_row_blocks<128>() * pj;
   a.n_pb = (int32_t)((seq_len + rows_per_block - 1) / rows_per_block);
   a.scale_log2 = sm_scale * kLog2e;
+  a.rcos = rq.cos; a.rsin = rq.sin; a.rpos = rq.pos;
+  a.r_ss = rq.row_stride; a.r_rows = rq.rows;
   const int nwaves = gh * pj;
   const int64_t blocks = (int64_t)a.B * a.Hkv * a.head_chunks * a.n_pb;
   if (blocks > INT32_MAX) {
@@ -1022,4 +1067,58 @@ extern "C" int32_t mi_attn_prefill(const void* q, const void* k, const void* v,
     return (int32_t)e;
   }
   return MI_OK;
+}
+
+}  // namespace
+
+extern "C" int32_t mi_attn_prefill(const void* q, const void* k, const void* v,
+                                   void* o, float* lse, int64_t batch,
+                                   int64_t n_heads, int64_t n_kv_heads,
+                                   int64_t seq_len, int64_t kv_len,
+                                   int64_t head_dim, int64_t q_sb, int64_t q_sh,
+                                   int64_t q_ss, int64_t k_sb, int64_t k_sh,
+                                   int64_t k_ss, int64_t v_sb, int64_t v_sh,
+                                   int64_t v_ss, int64_t o_sb, int64_t o_sh,
+                                   int64_t o_ss, float sm_scale, int32_t dtype,
+                                   void* stream) {
+  return attn_prefill(q, k, v, o, lse, batch, n_heads, n_kv_heads, seq_len, kv_len, head_dim,
+                      q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss, o_sb, o_sh, o_ss,
+                      sm_scale, dtype, RopeQ{}, stream);
+}
+
+extern "C" int32_t mi_attn_prefill_rope(
+    const void* q, const void* k, const void* v, void* o, float* lse, int64_t batch,
+    int64_t n_heads, int64_t n_kv_heads, int64_t seq_len, int64_t kv_len, int64_t head_dim,
+    int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+    int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb, int64_t o_sh, int64_t o_ss,
+    float sm_scale, const void* cos, const void* sin, int64_t table_rows,
+    int64_t table_row_stride, const int64_t* positions, int32_t dtype, void* stream) {
+  if (dtype != MI_DTYPE_BF16 && dtype != MI_DTYPE_F16) {
+    set_last_error("attn_prefill_rope: q RoPE is fused for bf16 / fp16 only (dtype code %d)",
+                   (int)dtype);
+    return MI_ERR_UNSUPPORTED;
+  }
+  if (cos == nullptr || sin == nullptr) {
+    set_last_error("attn_prefill_rope: null cos/sin table");
+    return MI_ERR_INVALID;
+  }
+  // rows of D/2 entries, 16-byte aligned (each lane reads 8 consecutive ones)
+  if (table_rows <= 0 || table_row_stride < head_dim / 2 || (table_row_stride * 2) % 16 != 0 ||
+      ((uintptr_t)cos | (uintptr_t)sin) % 16 != 0) {
+    set_last_error("attn_prefill_rope: cos/sin tables must hold rows of head_dim/2 entries with "
+                   "16-byte aligned rows (rows %lld, row stride %lld)",
+                   (long long)table_rows, (long long)table_row_stride);
+    return MI_ERR_INVALID;
+  }
+  if (positions == nullptr && table_rows < seq_len) {
+    set_last_error("attn_prefill_rope: %lld table rows for %lld query rows",
+                   (long long)table_rows, (long long)seq_len);
+    return MI_ERR_INVALID;
+  }
+  RopeQ rq;
+  rq.cos = cos; rq.sin = sin; rq.pos = positions;
+  rq.row_stride = table_row_stride; rq.rows = table_rows;
+  return attn_prefill(q, k, v, o, lse, batch, n_heads, n_kv_heads, seq_len, kv_len, head_dim,
+                      q_sb, q_sh, q_ss, k_sb, k_sh, k_ss, v_sb, v_sh, v_ss, o_sb, o_sh, o_ss,
+                      sm_scale, dtype, rq, stream);
 }

@@ -12,6 +12,8 @@
 // One thread per rotation pair (i, i + D/2); consecutive threads take
 // consecutive i, so loads/stores of a row coalesce when the head dim has unit
 // stride.  With cos == sin == NULL the append copies K unrotated (KV write).
+#include <initializer_list>
+
 #include "common.hpp"
 
 namespace mi {
@@ -27,19 +29,6 @@ struct RopeArgs {
   int64_t c_ss, c_sd, s_ss, s_sd;
   int32_t B, H, S, half;
 };
-
-template <typename T, typename CT>
-__device__ inline void rotate(float x1, float x2, CT cv, CT sv, T& y1, T& y2) {
-  // No contraction: products and the sum are each rounded to fp32, then the
-  // result is rounded to T (an fma, or a fused fma_mix f16 conversion, would
-  // round once and can differ in the last bit).
-#pragma clang fp contract(off)
-  const float c = Elem<CT>::to_f32(cv), s = Elem<CT>::to_f32(sv);
-  const float x1c = x1 * c, x2s = x2 * s, x2c = x2 * c, x1s = x1 * s;
-  const float r1 = x1c - x2s, r2 = x2c + x1s;
-  y1 = Elem<T>::from_f32(r1);
-  y2 = Elem<T>::from_f32(r2);
-}
 
 template <typename T, typename CT>
 __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
@@ -59,7 +48,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     const float x1 = Elem<T>::to_f32(xp[i * a.x_sd]);
     const float x2 = Elem<T>::to_f32(xp[(i + a.half) * a.x_sd]);
     T y1, y2;
-    rotate<T, CT>(x1, x2, *cp, *sp, y1, y2);
+    rope_rotate<T, CT>(x1, x2, *cp, *sp, y1, y2);
     op[i * a.o_sd] = y1;
     op[(i + a.half) * a.o_sd] = y2;
   }
@@ -107,7 +96,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvAppendArgs a) {
       const float x1 = Elem<T>::to_f32(kp[i * a.xk_sd]);
       const float x2 = Elem<T>::to_f32(kp[(i + a.half) * a.xk_sd]);
       T y1, y2;
-      rotate<T, CT>(x1, x2, *cp, *sp, y1, y2);
+      rope_rotate<T, CT>(x1, x2, *cp, *sp, y1, y2);
       kc[i * a.ck_sd] = y1;
       kc[(i + a.half) * a.ck_sd] = y2;
     } else {  // plain KV write (KVCache.update): K copied bitwise too
@@ -119,10 +108,116 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvAppendArgs a) {
   }
 }
 
+// 16-byte forms of the two kernels above for 2-byte data with tables in the
+// same dtype, unit head-dim strides and 16-byte aligned rows: a thread rotates
+// 8 consecutive pairs (i0 .. i0+7 with their partners i0+D/2 ..), one 16-byte
+// load or store per 8 elements.  Same per-pair arithmetic (rope_rotate), so the
+// same bits.
+template <typename T>
+__device__ inline void rotate8(const u32x4& xa, const u32x4& xb, const u32x4& cw,
+                               const u32x4& sw, u32x4& ya, u32x4& yb) {
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  const t8 x1 = __builtin_bit_cast(t8, xa), x2 = __builtin_bit_cast(t8, xb);
+  const t8 c = __builtin_bit_cast(t8, cw), sn = __builtin_bit_cast(t8, sw);
+  t8 y1, y2;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    T r1, r2;
+    rope_rotate<T, T>(Elem<T>::to_f32(x1[e]), Elem<T>::to_f32(x2[e]), c[e], sn[e], r1, r2);
+    y1[e] = r1;
+    y2[e] = r2;
+  }
+  ya = __builtin_bit_cast(u32x4, y1);
+  yb = __builtin_bit_cast(u32x4, y2);
+}
+
+// Grid: x over (token, 8-pair group) of one (batch, head) row, y over
+// (batch, head); 32-bit index arithmetic (the host checks the sizes).
+template <typename T>
+__global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a) {
+  const uint32_t nj = (uint32_t)a.half >> 3, per_row = (uint32_t)a.S * nj;
+  for (uint32_t bh = blockIdx.y; bh < (uint32_t)(a.B * a.H); bh += gridDim.y) {
+    const int b = (int)(bh / (uint32_t)a.H), h = (int)(bh % (uint32_t)a.H);
+    for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < per_row;
+         t += gridDim.x * blockDim.x) {
+      const int s = (int)(t / nj), i0 = 8 * (int)(t % nj);
+      const T* xp = reinterpret_cast<const T*>(a.x) + b * a.x_sb + h * a.x_sh + s * a.x_ss + i0;
+      T* op = reinterpret_cast<T*>(a.out) + b * a.o_sb + h * a.o_sh + s * a.o_ss + i0;
+      const int64_t crow = a.positions != nullptr ? a.positions[s] : s;
+      const T* cp = reinterpret_cast<const T*>(a.cos) + crow * a.c_ss + i0;
+      const T* sp = reinterpret_cast<const T*>(a.sin) + crow * a.s_ss + i0;
+      u32x4 ya, yb;
+      rotate8<T>(load16(xp), load16(xp + a.half), load16(cp), load16(sp), ya, yb);
+      *reinterpret_cast<u32x4*>(op) = ya;
+      *reinterpret_cast<u32x4*>(op + a.half) = yb;
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void rope_kv_append_vec_kernel(KvAppendArgs a) {
+  const uint32_t nj = (uint32_t)a.half >> 3, per_row = (uint32_t)a.S * nj;
+  for (uint32_t bh = blockIdx.y; bh < (uint32_t)(a.B * a.H); bh += gridDim.y) {
+    const int b = (int)(bh / (uint32_t)a.H), h = (int)(bh % (uint32_t)a.H);
+    for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < per_row;
+         t += gridDim.x * blockDim.x) {
+      const int s = (int)(t / nj), i0 = 8 * (int)(t % nj);
+      const int64_t pos = a.positions != nullptr ? a.positions[s] : a.start_pos + s;
+      if (pos < 0 || pos >= a.capacity) continue;
+      const T* kp = reinterpret_cast<const T*>(a.xk) + b * a.xk_sb + h * a.xk_sh + s * a.xk_ss + i0;
+      const T* vp = reinterpret_cast<const T*>(a.xv) + b * a.xv_sb + h * a.xv_sh + s * a.xv_ss + i0;
+      T* kc = reinterpret_cast<T*>(a.ck) + b * a.ck_sb + h * a.ck_sh + pos * a.ck_st + i0;
+      T* vc = reinterpret_cast<T*>(a.cv) + b * a.cv_sb + h * a.cv_sh + pos * a.cv_st + i0;
+      const u32x4 k1 = load16(kp), k2 = load16(kp + a.half);
+      const u32x4 v1 = load16(vp), v2 = load16(vp + a.half);
+      if (a.cos != nullptr) {
+        const int64_t crow = a.cos_by_pos ? pos : s;
+        const T* cp = reinterpret_cast<const T*>(a.cos) + crow * a.c_ss + i0;
+        const T* sp = reinterpret_cast<const T*>(a.sin) + crow * a.s_ss + i0;
+        u32x4 ya, yb;
+        rotate8<T>(k1, k2, load16(cp), load16(sp), ya, yb);
+        *reinterpret_cast<u32x4*>(kc) = ya;
+        *reinterpret_cast<u32x4*>(kc + a.half) = yb;
+      } else {  // plain KV write: K copied bitwise too
+        *reinterpret_cast<u32x4*>(kc) = k1;
+        *reinterpret_cast<u32x4*>(kc + a.half) = k2;
+      }
+      *reinterpret_cast<u32x4*>(vc) = v1;
+      *reinterpret_cast<u32x4*>(vc + a.half) = v2;
+    }
+  }
+}
+
 namespace {
 
 bool valid_dtype(int32_t d) {
   return d == MI_DTYPE_BF16 || d == MI_DTYPE_F16 || d == MI_DTYPE_F32;
+}
+
+// The 16-byte kernels apply: 2-byte data with tables of the same dtype, head_dim
+// a multiple of 16, unit head-dim strides, 16-byte aligned bases and rows.
+bool vec_ok(int32_t dtype, int32_t cdtype, int64_t head_dim, int64_t n_rows, int64_t seq_len,
+            std::initializer_list<const void*> ptrs,
+            std::initializer_list<int64_t> unit, std::initializer_list<int64_t> strides) {
+  if (dtype != cdtype || (dtype != MI_DTYPE_BF16 && dtype != MI_DTYPE_F16)) return false;
+  if (head_dim % 16 != 0) return false;
+  if (n_rows > INT32_MAX || seq_len * (head_dim / 16) > INT32_MAX) return false;
+  for (const void* p : ptrs)
+    if (p != nullptr && (uintptr_t)p % 16 != 0) return false;
+  for (int64_t u : unit)
+    if (u != 1) return false;
+  for (int64_t r : strides)
+    if ((r * 2) % 16 != 0) return false;
+  return true;
+}
+
+// (x, y) grid of the 16-byte kernels: y over the batch x head rows, x over a
+// row's tokens x 8-pair groups, both capped (the kernels loop over the rest).
+dim3 vec_grid(int64_t rows, int64_t per_row) {
+  int64_t gx = (per_row + 255) / 256, gy = rows;
+  if (gx > 4096) gx = 4096;
+  if (gy > 65535) gy = 65535;
+  return dim3((unsigned)(gx < 1 ? 1 : gx), (unsigned)(gy < 1 ? 1 : gy));
 }
 
 unsigned grid_for(int64_t total) {
@@ -190,7 +285,16 @@ extern "C" int32_t mi_rope(const void* x, void* out, const void* cos,
   a.c_ss = c_ss; a.c_sd = c_sd; a.s_ss = s_ss; a.s_sd = s_sd;
   a.B = (int32_t)batch; a.H = (int32_t)n_heads; a.S = (int32_t)seq_len;
   a.half = (int32_t)(head_dim / 2);
-  MI_ROPE_DISPATCH(rope_kernel, a, total, (hipStream_t)stream);
+  if (vec_ok(dtype, cdtype, head_dim, batch * n_heads, seq_len, {x, out, cos, sin}, {x_sd, o_sd, c_sd, s_sd},
+             {x_sb, x_sh, x_ss, o_sb, o_sh, o_ss, c_ss, s_ss})) {
+    const dim3 grid = vec_grid(batch * n_heads, seq_len * (head_dim / 16)), block(256);
+    if (dtype == MI_DTYPE_BF16)
+      hipLaunchKernelGGL(rope_vec_kernel<bf16_t>, grid, block, 0, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL(rope_vec_kernel<f16_t>, grid, block, 0, (hipStream_t)stream, a);
+  } else {
+    MI_ROPE_DISPATCH(rope_kernel, a, total, (hipStream_t)stream);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_last_error("rope: launch failed: %s", hipGetErrorString(e));
@@ -244,7 +348,19 @@ extern "C" int32_t mi_rope_kv_append(
   a.B = (int32_t)batch; a.H = (int32_t)n_kv_heads; a.S = (int32_t)seq_len;
   a.half = (int32_t)(head_dim / 2);
   a.cos_by_pos = cos_by_position;
-  MI_ROPE_DISPATCH(rope_kv_append_kernel, a, total, (hipStream_t)stream);
+  if (vec_ok(dtype, cos == nullptr ? dtype : cdtype, head_dim, batch * n_kv_heads, seq_len,
+             {xk, xv, cache_k, cache_v, cos, sin},
+             {xk_sd, xv_sd, ck_sd, cv_sd, cos == nullptr ? 1 : c_sd, cos == nullptr ? 1 : s_sd},
+             {xk_sb, xk_sh, xk_ss, xv_sb, xv_sh, xv_ss, ck_sb, ck_sh, ck_st, cv_sb, cv_sh, cv_st,
+              cos == nullptr ? 0 : c_ss, cos == nullptr ? 0 : s_ss})) {
+    const dim3 grid = vec_grid(batch * n_kv_heads, seq_len * (head_dim / 16)), block(256);
+    if (dtype == MI_DTYPE_BF16)
+      hipLaunchKernelGGL(rope_kv_append_vec_kernel<bf16_t>, grid, block, 0, (hipStream_t)stream, a);
+    else
+      hipLaunchKernelGGL(rope_kv_append_vec_kernel<f16_t>, grid, block, 0, (hipStream_t)stream, a);
+  } else {
+    MI_ROPE_DISPATCH(rope_kv_append_kernel, a, total, (hipStream_t)stream);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     set_last_error("rope_kv_append: launch failed: %s", hipGetErrorString(e));

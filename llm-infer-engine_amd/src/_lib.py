@@ -91,6 +91,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i64, _i64, _i64,                      # out strides
         _f32, _i32, _ptr,                      # sm_scale dtype stream
     ]),
+    "mi_attn_prefill_rope": (_i32, [
+        _ptr, _ptr, _ptr, _ptr, _ptr,          # q k v out lse
+        _i64, _i64, _i64, _i64, _i64, _i64,    # B Hq Hkv S L D
+        _i64, _i64, _i64,                      # q strides (b, h, s)
+        _i64, _i64, _i64,                      # k strides
+        _i64, _i64, _i64,                      # v strides
+        _i64, _i64, _i64,                      # out strides
+        _f32,                                  # sm_scale
+        _ptr, _ptr, _i64, _i64, _ptr,          # cos sin table_rows row_stride positions
+        _i32, _ptr,                            # dtype stream
+    ]),
     "mi_rope": (_i32, [
         _ptr, _ptr, _ptr, _ptr, _ptr,          # x out cos sin positions
         _i64, _i64, _i64, _i64,

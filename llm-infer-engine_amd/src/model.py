@@ -73,10 +73,12 @@ class Attention(nn.Module):
         xv = xv.view(batch_size, query_len, self.n_kv_heads, self.head_dim).transpose(1, 2)
 
         positions = scatter_positions if (use_cuda_graph and scatter_positions is not None) else None
-        torch.cuda.nvtx.range_push("RoPE")
-        xq = apply_rotary(xq, rope_cos, rope_sin,
-                          positions=positions if rope_by_position else None)
-        torch.cuda.nvtx.range_pop()
+        q_positions = positions if rope_by_position else None
+        if query_len == 1:
+            torch.cuda.nvtx.range_push("RoPE")
+            xq = apply_rotary(xq, rope_cos, rope_sin, positions=q_positions)
+            torch.cuda.nvtx.range_pop()
+        # (prefill: q's RoPE runs inside the attention kernel, flash_attention below)
 
         if kv_cache is not None:
             torch.cuda.nvtx.range_push("KV_cache")
@@ -90,7 +92,8 @@ class Attention(nn.Module):
 
         if query_len > 1:
             torch.cuda.nvtx.range_push("FlashAttn")
-            output = flash_attention(xq, xk, xv)
+            output = flash_attention(xq, xk, xv, rope_cos=rope_cos, rope_sin=rope_sin,
+                                     rope_positions=q_positions)
             torch.cuda.nvtx.range_pop()
         else:
             torch.cuda.nvtx.range_push("FlashDecode")

@@ -88,6 +88,38 @@ def test_rope_kv_append_rejects_out_of_capacity():
     assert st == -1 and "capacity" in _lib.last_error()
 
 
+def _prefill_rope_call(lib, **over):
+    a = dict(q=1 << 20, k=1 << 21, v=1 << 22, o=1 << 23, B=1, Hq=8, Hkv=2, S=64, L=64, D=64,
+             cos=1 << 24, sin=1 << 25, rows=64, rs=32, pos=None, dtype=0)
+    a.update(over)
+    D = a["D"]
+    return lib.mi_attn_prefill_rope(a["q"], a["k"], a["v"], a["o"], None, a["B"], a["Hq"],
+                                    a["Hkv"], a["S"], a["L"], D, a["Hq"] * a["S"] * D,
+                                    a["S"] * D, D, a["Hkv"] * a["L"] * D, a["L"] * D, D,
+                                    a["Hkv"] * a["L"] * D, a["L"] * D, D,
+                                    a["Hq"] * a["S"] * D, a["S"] * D, D, 0.125,
+                                    a["cos"], a["sin"], a["rows"], a["rs"], a["pos"],
+                                    a["dtype"], None)
+
+
+# every case is rejected before a launch (the pointers are not device memory)
+@pytest.mark.parametrize("over,code,msg", [
+    ({"dtype": 2}, -2, "bf16 / fp16"),
+    ({"cos": None}, -1, "null"),
+    ({"rows": 0}, -1, "rows"),
+    ({"rs": 16}, -1, "head_dim/2"),
+    ({"sin": (1 << 25) + 4}, -1, "aligned"),
+    ({"rows": 32}, -1, "table rows"),
+    ({"D": 96, "rs": 48}, -2, "head_dim"),
+    ({"Hq": 6, "Hkv": 4}, -1, "divisible"),
+])
+def test_prefill_rope_c_side_validation(over, code, msg):
+    from src import _lib
+    lib = _lib.load()
+    assert _prefill_rope_call(lib, **over) == code
+    assert msg in _lib.last_error()
+
+
 def _lm_head_call(lib, **over):
     a = dict(x=1 << 20, x_sm=2048, norm=None, eps=1e-5, w=1 << 21, w_sn=2048, y=1 << 22,
              y_sm=1000, tok=None, pv=None, pi=None, n_parts=0, m=8, n=1000, k=2048, dtype=0)

@@ -101,3 +101,60 @@ def test_config2_full_size(dev):
         ref, ref_lse = ora.prefill(q[b:b + 1], k[b:b + 1], v[b:b + 1], sm_scale=1.0)
         assert max_abs(out[b:b + 1], ref) < 2e-2
         assert max_abs(lse[b:b + 1], ref_lse) < 1e-3
+
+
+def _rope_tables(D, T, dtype, dev):
+    from src.rope import build_rope_cos_sin, precompute_freqs_cis
+    return build_rope_cos_sin(precompute_freqs_cis(D, T, theta=500000.0), dtype, dev)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("by_position", [False, True])
+def test_fused_q_rope_is_bitwise_apply_rotary_then_attention(dev, dtype, D, by_position):
+    """flash_attention(q, k, v, rope_cos=..., rope_sin=...) rotates q inside the
+    kernel: the same bits as apply_rotary(q) followed by flash_attention, in the
+    model layout (q a view of [B,S,H,D] memory, k/v cache views), and the
+    oracle's RoPE + prefill within the usual bars."""
+    from src.rope import apply_rotary
+    B, Hq, Hkv, S, T = 2, 16, 4, 203, 512
+    q = randn((B, S, Hq, D), 40, dtype, dev).transpose(1, 2)
+    kc = randn((B, Hkv, T, D), 41, dtype, dev)
+    vc = randn((B, Hkv, T, D), 42, dtype, dev)
+    k, v = kc[:, :, :S], vc[:, :, :S]
+    cos, sin = _rope_tables(D, T, dtype, dev)
+    if by_position:   # full tables, token s at position pos[s] (graph-runner style)
+        pos = torch.randperm(T, generator=torch.Generator().manual_seed(3))[:S].to(dev)
+        c_, s_, kw = cos, sin, dict(positions=pos)
+        ref_q = apply_rotary(q, cos, sin, positions=pos)
+        fused = _fa()(q, k, v, return_lse=True, rope_cos=cos, rope_sin=sin, rope_positions=pos)
+        oc, os_ = cos.cpu()[pos.cpu()], sin.cpu()[pos.cpu()]
+    else:             # tables sliced at the start position, row s for token s
+        c_, s_ = cos[37:37 + S], sin[37:37 + S]
+        ref_q = apply_rotary(q, c_, s_)
+        fused = _fa()(q, k, v, return_lse=True, rope_cos=c_, rope_sin=s_)
+        oc, os_ = c_.cpu(), s_.cpu()
+    sep = _fa()(ref_q, k, v, return_lse=True)
+    assert fused[0].stride() == q.stride()
+    assert torch.equal(fused[0], sep[0]) and torch.equal(fused[1], sep[1])
+    rq = orope.rotate(q.cpu(), oc, os_)
+    assert torch.equal(ref_q.cpu(), rq)
+    ref, ref_lse = ora.prefill(rq, k, v)
+    assert max_abs(fused[0], ref) < TOL[dtype]
+    assert max_abs(fused[1], ref_lse) < 1e-3
+
+
+def test_fused_q_rope_falls_back_where_the_kernel_does_not_rotate(dev):
+    """fp32 q, or tables of another dtype: flash_attention applies apply_rotary
+    first (same result as doing it by hand)."""
+    from src.rope import apply_rotary
+    for dtype, tdtype in ((torch.float32, torch.float32), (torch.bfloat16, torch.float32)):
+        q = randn((1, 8, 70, 64), 50, dtype, dev)
+        k = randn((1, 2, 70, 64), 51, dtype, dev)
+        v = randn((1, 2, 70, 64), 52, dtype, dev)
+        cos, sin = _rope_tables(64, 70, tdtype, dev)
+        a = _fa()(q, k, v, rope_cos=cos, rope_sin=sin)
+        b = _fa()(apply_rotary(q, cos, sin), k, v)
+        assert torch.equal(a, b)
+    with pytest.raises(ValueError, match="rows"):
+        _fa()(q, k, v, rope_cos=cos[:10], rope_sin=sin[:10])

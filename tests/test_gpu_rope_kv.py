@@ -121,3 +121,38 @@ def test_kvcache_update_and_update_positions(dev):
     for i, p in enumerate(pos.tolist()):
         assert torch.equal(kv.k[1, :, :, p], k3[:, :, i])
         assert torch.equal(kv.v[1, :, :, p], v3[:, :, i])
+
+
+@pytest.mark.parametrize("dtype,tdtype", [(torch.bfloat16, torch.float32),
+                                          (torch.float16, torch.float16),
+                                          (torch.float16, torch.float32)])
+def test_apply_rotary_positions_and_mixed_tables_bitwise(dev, dtype, tdtype):
+    """Tables by absolute position (device positions), the 16-byte path
+    (same-dtype tables) and the per-element path (fp32 tables) alike."""
+    from src.rope import apply_rotary
+    B, S, H, D, T = 2, 29, 4, 128, 200
+    x = randn((B, S, H, D), 60, dtype, dev).transpose(1, 2)
+    _, cos, sin = _tables(D, T, tdtype, dev)
+    pos = torch.randperm(T, generator=torch.Generator().manual_seed(1))[:S].to(dev)
+    out = apply_rotary(x, cos, sin, positions=pos)
+    ref = orope.rotate(x, cos.cpu()[pos.cpu()], sin.cpu()[pos.cpu()])
+    assert torch.equal(out.cpu(), ref)
+
+
+def test_rope_and_cache_update_fp16_and_unaligned_fallback(dev):
+    """fp16 through the 16-byte path; a head_dim of 40 (not a multiple of 16)
+    through the per-element path; both bitwise against the oracle."""
+    from src.rope import rope_and_cache_update
+    for dtype, D in ((torch.float16, 64), (torch.bfloat16, 40)):
+        n_layers, B, H, T, S, start = 2, 2, 4, 96, 33, 9
+        kv = _cache(n_layers, B, H, T, D, dtype, dev)
+        before_k, before_v = kv.k.cpu().clone(), kv.v.cpu().clone()
+        xk = randn((B, S, H, D), 70, dtype, dev).transpose(1, 2)
+        xv = randn((B, S, H, D), 71, dtype, dev).transpose(1, 2)
+        _, cos, sin = _tables(D, T, dtype, dev)
+        rope_and_cache_update(xk, xv, cos[start:start + S], sin[start:start + S], kv, 0,
+                              start_pos=start)
+        ref_k, ref_v = orope.rope_kv_append(before_k, before_v, 0, xk, xv,
+                                            cos[start:start + S], sin[start:start + S],
+                                            start_pos=start)
+        assert torch.equal(kv.k.cpu(), ref_k) and torch.equal(kv.v.cpu(), ref_v)
