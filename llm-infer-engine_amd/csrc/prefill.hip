@@ -128,8 +128,9 @@ __device__ inline int perm_row(int r) {
 // contiguously, lane t at +16t, so the swizzle is realised by choosing which
 // logical chunk each lane fetches.
 template <int D>
-__device__ inline int k_swz(int r) {  // XOR mask for K row r
-  if constexpr (D == 64) return (r >> 1) & 7;
+__device__ inline int k_swz(int r) {  // XOR mask for K row r (< the row's chunk count)
+  if constexpr (D == 32) return (r >> 1) & 3;
+  else if constexpr (D == 64) return (r >> 1) & 7;
   else return r & 15;
 }
 __device__ inline int v_swz(int r) { return (r >> 1) & 3; }  // XOR mask for V row r
@@ -994,9 +995,9 @@ int32_t attn_prefill(const void* q, const void* k, const void* v, void* o, float
     set_last_error("attn_prefill: unknown dtype code %d", (int)dtype);
     return MI_ERR_INVALID;
   }
-  if (head_dim != 64 && head_dim != 128) {
-    set_last_error("attn_prefill: head_dim %lld has no kernel (supported: 64, 128)",
-                   (long long)head_dim);
+  if (!(head_dim == 64 || head_dim == 128 || (head_dim == 32 && dtype != MI_DTYPE_F32))) {
+    set_last_error("attn_prefill: head_dim %lld has no kernel (supported: 64, 128; 32 for "
+                   "bf16/fp16)", (long long)head_dim);
     return MI_ERR_UNSUPPORTED;
   }
   const int64_t eb = dtype == MI_DTYPE_F32 ? 4 : 2;
@@ -1034,8 +1035,8 @@ int32_t attn_prefill(const void* q, const void* k, const void* v, void* o, float
   a.heads_per_block = gh;
   a.head_chunks = G / gh;
   a.pj = pj;
-  // D = 64 (16-bit): software-pipelined kernel, 4 waves of 64 rows; D = 128:
-  // 4 waves of 32 rows.
+  // D = 64 (16-bit): software-pipelined kernel, 4 waves of 64 rows; D = 32 and
+  // 128: 4 waves of 32 rows.
   const bool sp = head_dim == 64 && dtype != MI_DTYPE_F32;
   const int rows_per_block = sp ? 64 * pj : 32 * prefill_row_blocks<128>() * pj;
   a.n_pb = (int32_t)((seq_len + rows_per_block - 1) / rows_per_block);
@@ -1058,10 +1059,13 @@ int32_t attn_prefill(const void* q, const void* k, const void* v, void* o, float
     else
       hipLaunchKernelGGL(prefill_f32_kernel<128>, dim3((unsigned)nblk), dim3(256), 0, st, a);
     e = hipGetLastError();
-  } else if (dtype == MI_DTYPE_BF16)
-    e = sp ? launch_sp<bf16_t>(a, st) : launch<bf16_t, 128>(a, nwaves, st);
-  else
-    e = sp ? launch_sp<f16_t>(a, st) : launch<f16_t, 128>(a, nwaves, st);
+  } else if (dtype == MI_DTYPE_BF16) {
+    e = sp ? launch_sp<bf16_t>(a, st)
+           : head_dim == 32 ? launch<bf16_t, 32>(a, nwaves, st) : launch<bf16_t, 128>(a, nwaves, st);
+  } else {
+    e = sp ? launch_sp<f16_t>(a, st)
+           : head_dim == 32 ? launch<f16_t, 32>(a, nwaves, st) : launch<f16_t, 128>(a, nwaves, st);
+  }
   if (e != hipSuccess) {
     set_last_error("attn_prefill: launch failed: %s", hipGetErrorString(e));
     return (int32_t)e;

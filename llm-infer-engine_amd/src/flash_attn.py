@@ -14,7 +14,7 @@ once in LDS for all query heads of a group.  Keyword-only extensions:
               bits of flash_attention(apply_rotary(q, c, s), k, v).  In bf16/fp16
               the rotation runs in the attention kernel's Q prologue (one launch,
               q never rewritten); fp32 runs apply_rotary first.
-bf16/fp16 run on MFMA (head_dim 64 or 128), fp32 on a VALU kernel.
+bf16/fp16 run on MFMA (head_dim 32, 64 or 128), fp32 on a VALU kernel (64 or 128).
 """
 from __future__ import annotations
 

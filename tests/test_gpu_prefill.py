@@ -39,6 +39,30 @@ def test_prefill_matches_oracle(dev, dtype, D, Hq, Hkv, S):
     assert max_abs(lse, ref_lse) < 1e-3
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("Hq,Hkv,S", [(8, 2, 77), (16, 16, 256), (4, 1, 130)])
+def test_prefill_head_dim_32(dev, dtype, Hq, Hkv, S):
+    """head_dim 32 (the reference kernel takes any power-of-two head_dim,
+    src/flash_attn.py:29-32), with q's RoPE fused and without."""
+    from src.rope import apply_rotary
+    B, D = 2, 32
+    q = randn((B, S, Hq, D), 80, dtype, dev).transpose(1, 2)
+    k = randn((B, Hkv, S, D), 81, dtype, dev)
+    v = randn((B, Hkv, S, D), 82, dtype, dev)
+    out, lse = _fa()(q, k, v, return_lse=True)
+    ref, ref_lse = ora.prefill(q, k, v)
+    assert max_abs(out, ref) < TOL[dtype] and max_abs(lse, ref_lse) < 1e-3
+    cos, sin = _rope_tables(D, S, dtype, dev)
+    fused = _fa()(q, k, v, rope_cos=cos, rope_sin=sin)
+    assert torch.equal(fused, _fa()(apply_rotary(q, cos, sin), k, v))
+
+
+def test_prefill_head_dim_32_fp32_is_unsupported(dev):
+    q = randn((1, 4, 16, 32), 83, torch.float32, dev)
+    with pytest.raises(NotImplementedError, match="head_dim"):
+        _fa()(q, q[:, :1], q[:, :1])
+
+
 def test_reference_selftest_shape(dev):
     """src/flash_attn.py:113-135: B2 H4 S128 D64 fp32 vs SDPA, atol=rtol=1e-3."""
     q = randn((2, 4, 128, 64), 10, torch.float32, dev)
