@@ -18,14 +18,29 @@ MI355X version changes:
     greedy token loop never waits on the host (main.py:259-260 syncs per token).
 All launches inside the graph are the HIP kernels of libmiattn.so plus the
 library GEMMs/elementwise ops of the model.
+
+A model whose forward does not take ``seq_lens`` (the reference's own Llama3,
+src/model.py:145-154) is captured the reference's way instead: a static
+``freqs_cis`` row and a static [1, 1, 1, max_seq_len] bool mask, both rewritten
+before each replay (src/cuda_graph.py:19-70); ``greedy`` needs the native form.
 """
 from __future__ import annotations
+
+import inspect
 
 import torch
 import torch.nn as nn
 
 from .config import ModelArgs
 from .kv_cache import KVCache
+
+
+def _accepts(fn, name: str) -> bool:
+    try:
+        params = inspect.signature(fn).parameters
+    except (TypeError, ValueError):
+        return False
+    return name in params or any(p.kind == p.VAR_KEYWORD for p in params.values())
 
 
 class CUDAGraphDecodeRunner:
@@ -49,9 +64,26 @@ class CUDAGraphDecodeRunner:
         self.static_logits = None
         self.static_tokens = None
         self.greedy = bool(greedy)
+        # native form (seq_lens, device RoPE rows) or the reference's (freqs row + mask)
+        self.native = _accepts(model.forward, "seq_lens")
+        if not self.native:
+            if self.greedy:
+                raise ValueError("greedy=True needs a model whose forward takes seq_lens and "
+                                 "greedy")
+            fc = model.freqs_cis
+            self.static_freqs_cis = torch.zeros((1, fc.shape[-1]), dtype=fc.dtype, device=device)
+            self.static_decode_mask = torch.zeros((1, 1, 1, model_args.max_seq_len),
+                                                  dtype=torch.bool, device=device)
+            self.static_decode_mask[..., 0] = True
+            self.static_freqs_cis.copy_(fc[:1].to(device))
         self._capture()
 
     def _forward(self):
+        if not self.native:
+            return self.model(self.static_input_token, kv_cache=self.kv_cache,
+                              freqs_cis=self.static_freqs_cis, use_cuda_graph=True,
+                              scatter_positions=self.static_scatter_positions,
+                              decode_attn_mask=self.static_decode_mask)
         out = self.model(self.static_input_token, kv_cache=self.kv_cache, use_cuda_graph=True,
                          scatter_positions=self.static_scatter_positions,
                          seq_lens=self.static_seq_lens, greedy=self.greedy)
@@ -82,6 +114,11 @@ class CUDAGraphDecodeRunner:
             self.static_input_token.fill_(int(token_id))
         self.static_scatter_positions.fill_(int(current_pos))
         self.static_seq_lens.fill_(int(current_pos) + 1)
+        if not self.native:
+            p = int(current_pos)
+            self.static_freqs_cis.copy_(self.model.freqs_cis[p:p + 1].to(self.device))
+            self.static_decode_mask.zero_()
+            self.static_decode_mask[..., :p + 1] = True
 
     def replay(self) -> torch.Tensor:
         self.graph.replay()
