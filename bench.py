@@ -501,9 +501,9 @@ def bench_prefill_cfg1(torch, steps: int, warmup: int) -> dict:
     cos, sin = build_rope_cos_sin(precompute_freqs_cis(64, 512), torch.float32, dev)
     flops = 4.0 * 32 * 512 * 512 * 64 / 2
 
-    def step():
-        return flash_attention(apply_rotary(q, cos, sin), apply_rotary(k, cos, sin), v,
-                               return_lse=True)
+    def step():   # q's RoPE inside the attention kernel, K's by apply_rotary
+        return flash_attention(q, apply_rotary(k, cos, sin), v, return_lse=True,
+                               rope_cos=cos, rope_sin=sin)
     _settle(torch, step, warmup)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)

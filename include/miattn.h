@@ -223,9 +223,9 @@ int32_t mi_attn_prefill(const void* q, const void* k, const void* v, void* out,
  * prologue (q is read unrotated and never written): query row s of every
  * head uses row positions[s] of cos/sin (clamped into [0, table_rows)), or
  * row s when positions is NULL.  cos/sin [table_rows, >= head_dim/2] in q's
- * dtype, unit column stride, 16-byte aligned rows of table_row_stride
- * elements.  bf16/fp16 only (fp32: mi_rope, then mi_attn_prefill).  The
- * result is bitwise that of mi_rope on q followed by mi_attn_prefill.
+ * dtype, unit column stride, rows of table_row_stride elements (16-byte
+ * aligned for bf16/fp16).  The result is bitwise that of mi_rope on q
+ * followed by mi_attn_prefill.
  * Replaces apply_rotary(xq) + flash_attention of one prefill step
  *   src/rope.py:48-119 (rope_kernel, apply_rotary), src/flash_attn.py:5-111,
  *   as called by src/model.py:62-79.

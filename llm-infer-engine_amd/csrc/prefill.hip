@@ -871,13 +871,18 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
   }
 }
 
-// fp32 inputs: plain VALU flash attention (no fp32 MFMA tiles), TPR = D/32
-// lanes per query row, 32 dims each; K/V tiles of 64 keys staged in LDS and
-// read as broadcasts.  Used for fp32 models (e.g. the CPU-shaped parity case).
+// fp32 inputs: plain VALU flash attention (no fp32 MFMA tiles).  TPR = D/16
+// lanes per query row, 16 dims each (64 rows per 256-thread block at D = 64,
+// 32 at D = 128, so even a short sequence gives the GPU a few hundred blocks);
+// K/V tiles staged in LDS and read as broadcasts.  Keys are taken 8 at a time:
+// 8 independent dot-product chains, one running-max update and one rescale per
+// group of 8.  Optional q RoPE in the prologue (the RoPE kernels' rounding).
+// Used for fp32 models (e.g. the CPU-shaped parity case).
 template <int D>
 __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillArgs a) {
-  constexpr int TPR = D / 32, BN = 4096 / D;  // K+V tiles stay at ~33 KB of LDS
+  constexpr int DL = 16, TPR = D / DL, BN = 4096 / D;  // K+V tiles stay at ~33 KB of LDS
   constexpr int ROWS = 256 / TPR;  // query rows per block
+  constexpr int KB = 8;            // keys per softmax update
   __shared__ float ks[BN][D + 1];
   __shared__ float vs[BN][D + 1];
   const int tid = threadIdx.x;
@@ -890,10 +895,26 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillArgs a) {
   const int qrow = rb * ROWS + row_in;
   const int qr = min(qrow, a.S - 1);
   const float* qp = reinterpret_cast<const float*>(a.q) + (int64_t)b * a.q_sb +
-                    (int64_t)head * a.q_sh + (int64_t)qr * a.q_ss + part * 32;
-  float qv[32], acc[32];
+                    (int64_t)head * a.q_sh + (int64_t)qr * a.q_ss;
+  float qv[DL], acc[DL];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) { qv[i] = qp[i]; acc[i] = 0.f; }
+  for (int i = 0; i < DL; ++i) { qv[i] = qp[part * DL + i]; acc[i] = 0.f; }
+  if (a.rcos != nullptr) {
+    // rotation partner of dim d is d + D/2 (or d - D/2): lane part +- TPR/2
+    int64_t crow = qr;
+    if (a.rpos != nullptr) crow = min(max(a.rpos[qr], (int64_t)0), a.r_rows - 1);
+    const bool lo = part < TPR / 2;
+    const int i0 = (lo ? part : part - TPR / 2) * DL;
+    const float* cp = reinterpret_cast<const float*>(a.rcos) + crow * a.r_ss + i0;
+    const float* sp = reinterpret_cast<const float*>(a.rsin) + crow * a.r_ss + i0;
+#pragma unroll
+    for (int i = 0; i < DL; ++i) {
+      const float other = qp[(lo ? part + TPR / 2 : part - TPR / 2) * DL + i];
+      float y1, y2;
+      rope_rotate<float, float>(lo ? qv[i] : other, lo ? other : qv[i], cp[i], sp[i], y1, y2);
+      qv[i] = lo ? y1 : y2;
+    }
+  }
   float m = kNegBig, l = 0.f;
   const float* kb = reinterpret_cast<const float*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh;
   const float* vb = reinterpret_cast<const float*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh;
@@ -908,25 +929,48 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillArgs a) {
     }
     __syncthreads();
     const int nk = min(BN, qrow - k0 + 1);  // keys k0..qrow are visible
-    for (int jj = 0; jj < nk; ++jj) {
-      float sdot = 0.f;
+    for (int j0 = 0; j0 < nk; j0 += KB) {
+      float sc[KB];
 #pragma unroll
-      for (int i = 0; i < 32; ++i) sdot = fmaf(qv[i], ks[jj][part * 32 + i], sdot);
-      sdot = group_sum<TPR>(sdot) * a.scale_log2;
-      const float mn = fmaxf(m, sdot);
-      const float alpha = fast_exp2(m - mn), p = fast_exp2(sdot - mn);
-      l = l * alpha + p;
+      for (int u = 0; u < KB; ++u) {
+        const int jj = min(j0 + u, BN - 1);
+        float sdot = 0.f;
 #pragma unroll
-      for (int i = 0; i < 32; ++i) acc[i] = fmaf(p, vs[jj][part * 32 + i], acc[i] * alpha);
+        for (int i = 0; i < DL; ++i) sdot = fmaf(qv[i], ks[jj][part * DL + i], sdot);
+        sc[u] = sdot;
+      }
+      float mx = kNegBig;
+#pragma unroll
+      for (int u = 0; u < KB; ++u) {
+        sc[u] = group_sum<TPR>(sc[u]) * a.scale_log2;
+        if (j0 + u >= nk) sc[u] = -INFINITY;
+        mx = fmaxf(mx, sc[u]);
+      }
+      const float mn = fmaxf(m, mx);
+      const float alpha = fast_exp2(m - mn);
+      float ps = 0.f, p[KB];
+#pragma unroll
+      for (int u = 0; u < KB; ++u) {
+        p[u] = fast_exp2(sc[u] - mn);
+        ps += p[u];
+      }
+      l = l * alpha + ps;
+#pragma unroll
+      for (int i = 0; i < DL; ++i) {
+        float t = acc[i] * alpha;
+#pragma unroll
+        for (int u = 0; u < KB; ++u) t = fmaf(p[u], vs[min(j0 + u, BN - 1)][part * DL + i], t);
+        acc[i] = t;
+      }
       m = mn;
     }
   }
   if (qrow >= a.S) return;
   float* op = reinterpret_cast<float*>(a.o) + (int64_t)b * a.o_sb + (int64_t)head * a.o_sh +
-              (int64_t)qrow * a.o_ss + part * 32;
+              (int64_t)qrow * a.o_ss + part * DL;
   const float inv = 1.0f / l;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) op[i] = acc[i] * inv;
+  for (int i = 0; i < DL; ++i) op[i] = acc[i] * inv;
   if (a.lse != nullptr && part == 0)
     a.lse[((int64_t)b * a.Hq + head) * a.S + qrow] = (m + __log2f(l)) * kLn2;
 }
@@ -1052,7 +1096,7 @@ int32_t attn_prefill(const void* q, const void* k, const void* v, void* o, float
   hipError_t e;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MI_DTYPE_F32) {
-    const int rows = 256 / (int)(head_dim / 32);
+    const int rows = 256 / (int)(head_dim / 16);
     const int64_t nblk = (int64_t)a.B * a.Hq * ((a.S + rows - 1) / rows);
     if (head_dim == 64)
       hipLaunchKernelGGL(prefill_f32_kernel<64>, dim3((unsigned)nblk), dim3(256), 0, st, a);
@@ -1097,18 +1141,18 @@ extern "C" int32_t mi_attn_prefill_rope(
     int64_t v_sb, int64_t v_sh, int64_t v_ss, int64_t o_sb, int64_t o_sh, int64_t o_ss,
     float sm_scale, const void* cos, const void* sin, int64_t table_rows,
     int64_t table_row_stride, const int64_t* positions, int32_t dtype, void* stream) {
-  if (dtype != MI_DTYPE_BF16 && dtype != MI_DTYPE_F16) {
-    set_last_error("attn_prefill_rope: q RoPE is fused for bf16 / fp16 only (dtype code %d)",
-                   (int)dtype);
-    return MI_ERR_UNSUPPORTED;
+  if (dtype != MI_DTYPE_BF16 && dtype != MI_DTYPE_F16 && dtype != MI_DTYPE_F32) {
+    set_last_error("attn_prefill_rope: unknown dtype code %d", (int)dtype);
+    return MI_ERR_INVALID;
   }
   if (cos == nullptr || sin == nullptr) {
     set_last_error("attn_prefill_rope: null cos/sin table");
     return MI_ERR_INVALID;
   }
-  // rows of D/2 entries, 16-byte aligned (each lane reads 8 consecutive ones)
-  if (table_rows <= 0 || table_row_stride < head_dim / 2 || (table_row_stride * 2) % 16 != 0 ||
-      ((uintptr_t)cos | (uintptr_t)sin) % 16 != 0) {
+  // rows of D/2 entries; 16-bit tables 16-byte aligned (a lane reads 8 at once)
+  const bool wide = dtype == MI_DTYPE_F32;
+  if (table_rows <= 0 || table_row_stride < head_dim / 2 ||
+      (!wide && ((table_row_stride * 2) % 16 != 0 || ((uintptr_t)cos | (uintptr_t)sin) % 16 != 0))) {
     set_last_error("attn_prefill_rope: cos/sin tables must hold rows of head_dim/2 entries with "
                    "16-byte aligned rows (rows %lld, row stride %lld)",
                    (long long)table_rows, (long long)table_row_stride);

@@ -11,9 +11,9 @@ once in LDS for all query heads of a group.  Keyword-only extensions:
   rope_cos, rope_sin, rope_positions
               apply the rotate-half RoPE of apply_rotary (src/rope.py) to q
               first: flash_attention(q, k, v, rope_cos=c, rope_sin=s) gives the
-              bits of flash_attention(apply_rotary(q, c, s), k, v).  In bf16/fp16
-              the rotation runs in the attention kernel's Q prologue (one launch,
-              q never rewritten); fp32 runs apply_rotary first.
+              bits of flash_attention(apply_rotary(q, c, s), k, v).  With tables
+              in q's dtype the rotation runs in the attention kernel's Q prologue
+              (one launch, q never rewritten); otherwise apply_rotary runs first.
 bf16/fp16 run on MFMA (head_dim 32, 64 or 128), fp32 on a VALU kernel (64 or 128).
 """
 from __future__ import annotations
@@ -62,12 +62,13 @@ def flash_attention(q, k, v, *, return_lse: bool = False, sm_scale: float | None
         elif rope_positions.numel() < seq_len:
             raise ValueError(f"flash_attention: {rope_positions.numel()} rope positions for "
                              f"{seq_len} queries")
-        fuse = (q.dtype in (torch.float16, torch.bfloat16) and rope_cos.dtype == q.dtype
-                and rope_cos.shape == rope_sin.shape and rope_cos.stride() == rope_sin.stride()
+        fuse = (rope_cos.dtype == q.dtype and rope_cos.shape == rope_sin.shape
+                and rope_cos.stride() == rope_sin.stride()
                 and rope_cos.dim() == 2 and rope_cos.stride(1) == 1
                 and rope_cos.shape[1] >= head_dim // 2
-                and (rope_cos.stride(0) * 2) % 16 == 0
-                and rope_cos.data_ptr() % 16 == 0 and rope_sin.data_ptr() % 16 == 0)
+                and (q.dtype == torch.float32
+                     or ((rope_cos.stride(0) * 2) % 16 == 0
+                         and rope_cos.data_ptr() % 16 == 0 and rope_sin.data_ptr() % 16 == 0)))
         if not fuse:
             q = apply_rotary(q, rope_cos, rope_sin, positions=rope_positions)
             rope = False

@@ -104,7 +104,7 @@ def _prefill_rope_call(lib, **over):
 
 # every case is rejected before a launch (the pointers are not device memory)
 @pytest.mark.parametrize("over,code,msg", [
-    ({"dtype": 2}, -2, "bf16 / fp16"),
+    ({"dtype": 5}, -1, "dtype"),
     ({"cos": None}, -1, "null"),
     ({"rows": 0}, -1, "rows"),
     ({"rs": 16}, -1, "head_dim/2"),

@@ -168,15 +168,17 @@ def test_fused_q_rope_is_bitwise_apply_rotary_then_attention(dev, dtype, D, by_p
     assert max_abs(fused[1], ref_lse) < 1e-3
 
 
-def test_fused_q_rope_falls_back_where_the_kernel_does_not_rotate(dev):
-    """fp32 q, or tables of another dtype: flash_attention applies apply_rotary
-    first (same result as doing it by hand)."""
+def test_fused_q_rope_fp32_and_mixed_tables(dev):
+    """fp32 q with fp32 tables (rotated in the fp32 kernel's prologue), and
+    tables of another dtype than q (apply_rotary first): the same bits as
+    apply_rotary by hand, for D 64 and 128."""
     from src.rope import apply_rotary
-    for dtype, tdtype in ((torch.float32, torch.float32), (torch.bfloat16, torch.float32)):
-        q = randn((1, 8, 70, 64), 50, dtype, dev)
-        k = randn((1, 2, 70, 64), 51, dtype, dev)
-        v = randn((1, 2, 70, 64), 52, dtype, dev)
-        cos, sin = _rope_tables(64, 70, tdtype, dev)
+    for dtype, tdtype, D in ((torch.float32, torch.float32, 64), (torch.float32, torch.float32, 128),
+                             (torch.bfloat16, torch.float32, 64)):
+        q = randn((1, 70, 8, D), 50, dtype, dev).transpose(1, 2)
+        k = randn((1, 2, 70, D), 51, dtype, dev)
+        v = randn((1, 2, 70, D), 52, dtype, dev)
+        cos, sin = _rope_tables(D, 70, tdtype, dev)
         a = _fa()(q, k, v, rope_cos=cos, rope_sin=sin)
         b = _fa()(apply_rotary(q, cos, sin), k, v)
         assert torch.equal(a, b)
