@@ -871,20 +871,22 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
   }
 }
 
-// fp32 inputs: plain VALU flash attention (no fp32 MFMA tiles).  TPR = D/16
-// lanes per query row, 16 dims each (64 rows per 256-thread block at D = 64,
-// 32 at D = 128, so even a short sequence gives the GPU a few hundred blocks);
-// K/V tiles staged in LDS and read as broadcasts.  Keys are taken 8 at a time:
-// 8 independent dot-product chains, one running-max update and one rescale per
-// group of 8.  Optional q RoPE in the prologue (the RoPE kernels' rounding).
-// Used for fp32 models (e.g. the CPU-shaped parity case).
+// fp32 inputs: plain VALU flash attention (no fp32 MFMA tiles).  TPR = D/8
+// lanes per query row, 8 dims each (32 rows per 256-thread block at D = 64,
+// 16 at D = 128, so a short sequence still gives the GPU hundreds of blocks
+// and a long row's chain of keys is split over many lanes); K/V tiles staged
+// in LDS with 16-byte copies and read back as 16-byte broadcasts.  Keys are
+// taken 8 at a time: 8 independent dot-product chains, one running-max update
+// and one rescale per group of 8.  Optional q RoPE in the prologue (the RoPE
+// kernels' rounding).  Used for fp32 models (e.g. the CPU-shaped parity case).
 template <int D>
 __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillArgs a) {
-  constexpr int DL = 16, TPR = D / DL, BN = 4096 / D;  // K+V tiles stay at ~33 KB of LDS
+  constexpr int DL = 8, TPR = D / DL, BN = 4096 / D;  // K+V tiles: 32 KB of LDS
   constexpr int ROWS = 256 / TPR;  // query rows per block
   constexpr int KB = 8;            // keys per softmax update
-  __shared__ float ks[BN][D + 1];
-  __shared__ float vs[BN][D + 1];
+  __shared__ __align__(16) float ks[BN][D];
+  __shared__ __align__(16) float vs[BN][D];
+  typedef float f4 __attribute__((ext_vector_type(4)));
   const int tid = threadIdx.x;
   const int part = tid % TPR, row_in = tid / TPR;
   const int n_rb = (a.S + ROWS - 1) / ROWS;
@@ -921,11 +923,11 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillArgs a) {
   const int last = min(rb * ROWS + ROWS, a.S) - 1;
   for (int k0 = 0; k0 <= last; k0 += BN) {
     __syncthreads();
-    for (int e = tid; e < BN * D; e += 256) {
-      const int r = e / D, d = e % D;
+    for (int e = tid; e < BN * D / 4; e += 256) {
+      const int r = e / (D / 4), d = 4 * (e % (D / 4));
       const int row = min(k0 + r, a.S - 1);
-      ks[r][d] = kb[(int64_t)row * a.k_ss + d];
-      vs[r][d] = vb[(int64_t)row * a.v_ss + d];
+      *reinterpret_cast<f4*>(&ks[r][d]) = *reinterpret_cast<const f4*>(kb + (int64_t)row * a.k_ss + d);
+      *reinterpret_cast<f4*>(&vs[r][d]) = *reinterpret_cast<const f4*>(vb + (int64_t)row * a.v_ss + d);
     }
     __syncthreads();
     const int nk = min(BN, qrow - k0 + 1);  // keys k0..qrow are visible
@@ -933,10 +935,13 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillArgs a) {
       float sc[KB];
 #pragma unroll
       for (int u = 0; u < KB; ++u) {
-        const int jj = min(j0 + u, BN - 1);
+        const float* kr = &ks[min(j0 + u, BN - 1)][part * DL];
+        const f4 k0v = *reinterpret_cast<const f4*>(kr), k1v = *reinterpret_cast<const f4*>(kr + 4);
         float sdot = 0.f;
 #pragma unroll
-        for (int i = 0; i < DL; ++i) sdot = fmaf(qv[i], ks[jj][part * DL + i], sdot);
+        for (int i = 0; i < 4; ++i) sdot = fmaf(qv[i], k0v[i], sdot);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sdot = fmaf(qv[4 + i], k1v[i], sdot);
         sc[u] = sdot;
       }
       float mx = kNegBig;
@@ -956,11 +961,15 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillArgs a) {
       }
       l = l * alpha + ps;
 #pragma unroll
-      for (int i = 0; i < DL; ++i) {
-        float t = acc[i] * alpha;
+      for (int i = 0; i < DL; ++i) acc[i] *= alpha;
 #pragma unroll
-        for (int u = 0; u < KB; ++u) t = fmaf(p[u], vs[min(j0 + u, BN - 1)][part * DL + i], t);
-        acc[i] = t;
+      for (int u = 0; u < KB; ++u) {
+        const float* vr = &vs[min(j0 + u, BN - 1)][part * DL];
+        const f4 v0 = *reinterpret_cast<const f4*>(vr), v1 = *reinterpret_cast<const f4*>(vr + 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = fmaf(p[u], v0[i], acc[i]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[4 + i] = fmaf(p[u], v1[i], acc[4 + i]);
       }
       m = mn;
     }
@@ -1096,7 +1105,7 @@ int32_t attn_prefill(const void* q, const void* k, const void* v, void* o, float
   hipError_t e;
   hipStream_t st = (hipStream_t)stream;
   if (dtype == MI_DTYPE_F32) {
-    const int rows = 256 / (int)(head_dim / 16);
+    const int rows = 256 / (int)(head_dim / 8);
     const int64_t nblk = (int64_t)a.B * a.Hq * ((a.S + rows - 1) / rows);
     if (head_dim == 64)
       hipLaunchKernelGGL(prefill_f32_kernel<64>, dim3((unsigned)nblk), dim3(256), 0, st, a);
