@@ -581,7 +581,8 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one plain 1 GiB device copy (scales rocprofv3 FETCH/WRITE_SIZE)")
-    ap.add_argument("--only", choices=["prefill", "decode", "step", "gemm", "load"], default=None,
+    ap.add_argument("--only", choices=["prefill", "prefill_model", "decode", "step", "gemm", "load"],
+                    default=None,
                     help="run one leg only (profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -607,6 +608,7 @@ def main() -> None:
     if args.only in (None, "prefill"):
         pre = bench_prefill(torch, args.steps, args.warmup)
         extra["prefill_config1"] = bench_prefill_cfg1(torch, args.steps, args.warmup)
+    if args.only in (None, "prefill_model"):
         extra["prefill_config2_model_layout"] = bench_prefill_model_layout(torch, args.steps,
                                                                            args.warmup)
     if args.only in (None, "decode"):
