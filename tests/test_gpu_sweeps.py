@@ -22,20 +22,44 @@ TOL = {torch.bfloat16: 2e-2, torch.float16: 5e-3}
 
 @pytest.mark.parametrize("seed", range(32))
 def test_prefill_random_shapes(dev, seed):
+    """Random shapes, head dims 32/64/128, q as a view of [B,S,H,D] memory or
+    contiguous, and (half the cases) q's RoPE fused into the kernel with the
+    table sliced at a random start row or indexed by random positions."""
     from src.flash_attn import flash_attention
+    from src.rope import build_rope_cos_sin, precompute_freqs_cis
+    from oracle import rope as orope
     rng = random.Random(1000 + seed)
     B = rng.randint(1, 3)
     Hkv = rng.choice([1, 2, 4, 8])
     G = rng.choice([1, 2, 3, 4, 6, 8])
-    D = rng.choice([64, 128])
+    D = rng.choice([32, 64, 128])
     S = rng.randint(1, 640)
     dtype = rng.choice([torch.bfloat16, torch.float16])
-    q = randn((B, Hkv * G, S, D), seed, dtype, dev)
+    bshd = rng.random() < 0.5
+    rope = rng.choice([None, "rows", "positions"])
+    Hq = Hkv * G
+    if bshd:
+        q = randn((B, S, Hq, D), seed, dtype, dev).transpose(1, 2)
+    else:
+        q = randn((B, Hq, S, D), seed, dtype, dev)
     k = randn((B, Hkv, S, D), seed + 1, dtype, dev)
     v = randn((B, Hkv, S, D), seed + 2, dtype, dev)
-    out, lse = flash_attention(q, k, v, return_lse=True)
-    ref, ref_lse = ora.prefill(q, k, v)
-    case = (B, Hkv, G, D, S, dtype)
+    kw, qref = {}, q.cpu()
+    if rope is not None:
+        T = S + 64
+        cos, sin = build_rope_cos_sin(precompute_freqs_cis(D, T, theta=500000.0), dtype, dev)
+        if rope == "rows":
+            r0 = rng.randint(0, 64)
+            c_, s_ = cos[r0:r0 + S], sin[r0:r0 + S]
+            kw = dict(rope_cos=c_, rope_sin=s_)
+            qref = orope.rotate(qref, c_.cpu(), s_.cpu())
+        else:
+            pos = torch.randperm(T, generator=torch.Generator().manual_seed(seed))[:S]
+            kw = dict(rope_cos=cos, rope_sin=sin, rope_positions=pos.to(dev))
+            qref = orope.rotate(qref, cos.cpu()[pos], sin.cpu()[pos])
+    out, lse = flash_attention(q, k, v, return_lse=True, **kw)
+    ref, ref_lse = ora.prefill(qref, k, v)
+    case = (B, Hkv, G, D, S, dtype, bshd, rope)
     assert max_abs(out, ref) < TOL[dtype], case
     assert max_abs(lse, ref_lse) < 1e-3, case
 
