@@ -204,21 +204,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   const int qpos0 = p0 + 32 * RB * j;     // first query row of this wave
   const bool wave_active = qpos0 < a.S;
 
-  // ---- Q as the B operand of S^T = K Q^T (lane: row lr of each row block)
+  // ---- Q as the B operand of S^T = K Q^T (lane: row lr of each row block),
+  //      loaded in the prologue after the first tile copy is issued
   v8 qreg[RB][DC];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int qrow = qpos0 + 32 * rb + lr;
-    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
-                  (int64_t)head * a.q_sh + (int64_t)min(qrow, a.S - 1) * a.q_ss;
-#pragma unroll
-    for (int c = 0; c < DC; ++c) {
-      u32x4 raw = load16(qp + 16 * c + 8 * hh);
-      if (qrow >= a.S) raw = u32x4{0, 0, 0, 0};
-      qreg[rb][c] = __builtin_bit_cast(v8, raw);
-    }
-    if (a.rcos != nullptr) rope_q_fragments<T, DC>(a, min(qrow, a.S - 1), hh, qreg[rb]);
-  }
 
   // ---- DMA geometry: wave w copies 1 KB pieces (w*NI + i) of each tile
   const unsigned char* kbase = reinterpret_cast<const unsigned char*>(a.k) +
@@ -291,7 +279,20 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   for (int rb = 0; rb < RB; ++rb) { m[rb] = kNegBig; l[rb] = 0.f; }
   const float sl2 = a.scale_log2;
 
+  // prologue: tile 0 in flight, then Q (and its RoPE table rows), so both
+  // share one memory round trip (loads complete in issue order, and the
+  // compiler's wait for Q covers the copy).  Rows past S read row S - 1:
+  // finite scores in rows whose output is never stored.
   issue(0, 0);
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int qrow = min(qpos0 + 32 * rb + lr, a.S - 1);
+    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                  (int64_t)head * a.q_sh + (int64_t)qrow * a.q_ss;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) qreg[rb][c] = __builtin_bit_cast(v8, load16(qp + 16 * c + 8 * hh));
+    if (a.rcos != nullptr) rope_q_fragments<T, DC>(a, qrow, hh, qreg[rb]);
+  }
   dma_wait_all();
   __syncthreads();
 
@@ -521,21 +522,9 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
   const int n_tw = r0 < a.S ? r0 / BN + 1 : 0;       // tiles this wave reads (last = diagonal)
   const int n_tiles = (min(p0 + 64 * PJ, a.S) - 1) / BN + 1;  // tiles the block copies
 
-  // ---- Q as the B operand of S^T = K Q^T (lane: row lr of each row block)
+  // ---- Q as the B operand of S^T = K Q^T (lane: row lr of each row block),
+  //      loaded in the prologue after the first tile copies are issued
   v8 qreg[2][DC];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
-    const int qrow = r0 + 32 * rb + lr;
-    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
-                  (int64_t)head * a.q_sh + (int64_t)min(qrow, a.S - 1) * a.q_ss;
-#pragma unroll
-    for (int c = 0; c < DC; ++c) {
-      u32x4 raw = load16(qp + 16 * c + 8 * hh);
-      if (qrow >= a.S) raw = u32x4{0, 0, 0, 0};
-      qreg[rb][c] = __builtin_bit_cast(v8, raw);
-    }
-    if (a.rcos != nullptr) rope_q_fragments<T, DC>(a, min(qrow, a.S - 1), hh, qreg[rb]);
-  }
 
   // ---- tile copies: wave w copies 1 KB pieces (w*NI + i) of each tile
   const unsigned char* kbase = reinterpret_cast<const unsigned char*>(a.k) +
@@ -813,10 +802,24 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
   };
   auto buf = [&](int t) { return lds + (t % kSpBufs) * SLOT_B; };
 
-  // ---- prologue: tiles 0..2 in flight, wait for tile 0, QK(0.h0)
+  // ---- prologue: tiles 0..2 in flight, then Q (and its RoPE table rows),
+  //      so the tile copies and the Q loads share one memory round trip (the
+  //      copies are issued first: loads complete in issue order, and the
+  //      compiler's wait for Q then covers them).  Rows past S read row S - 1:
+  //      finite scores in rows whose output is never stored (each row's
+  //      softmax and PV column are its own).  Wait for tile 0, QK(0.h0).
   issue(0);
   if (n_tiles > 1) issue(1);
   if (n_tiles > 2) issue(2);
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int qrow = min(r0 + 32 * rb + lr, a.S - 1);
+    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                  (int64_t)head * a.q_sh + (int64_t)qrow * a.q_ss;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) qreg[rb][c] = __builtin_bit_cast(v8, load16(qp + 16 * c + 8 * hh));
+    if (a.rcos != nullptr) rope_q_fragments<T, DC>(a, qrow, hh, qreg[rb]);
+  }
   wait_tiles(min(n_tiles - 1, 2));
   block_sync_lds();
   int t = 0;
