@@ -57,7 +57,34 @@ struct DecodeArgs {
   int32_t direct;     // num_splits == 1: normalise and write out/lse here
   int32_t empty_nan;  // empty rows -> NaN instead of 0
   int32_t q_vec;      // q rows are 16-byte aligned with unit d-stride
+  int32_t by_length;  // seq_lens given, 2 <= B <= 64: grid rows dealt by length
 };
+
+// Batch row served by grid row z when the sequences are dealt by length (a
+// bijection of [0, B)): the first ceil(B/2) grid rows take the sequences in
+// decreasing length, the others in increasing length.  The blocks of one
+// dispatch round fill the CUs in grid order, so the two blocks a CU receives
+// (grid rows z and z + ceil(B/2)) then pair a long sequence with a short one
+// instead of two arbitrary ones, and the CUs stream similar numbers of keys.
+// One lane per sequence (B <= 64); ties are broken by index.  Returns the
+// batch row and stores its seq_lens entry in *len.
+__device__ inline int length_ranked_batch(const int64_t* seq_lens, int B, int z, int lane,
+                                          int64_t* len) {
+  const int64_t my = lane < B ? seq_lens[lane] : 0;
+  int rank = 0;
+  for (int t = 0; t < B; ++t) {
+    const int64_t o = ((int64_t)__builtin_amdgcn_readlane((int)(my >> 32), t) << 32) |
+                      (uint32_t)__builtin_amdgcn_readlane((int)my, t);
+    rank += (o > my || (o == my && t < lane)) ? 1 : 0;
+  }
+  const int first = B - B / 2;
+  const int r = z < first ? z : B - 1 - (z - first);
+  const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < B && rank == r);
+  const int b = (int)__builtin_ctzll(hit);
+  *len = ((int64_t)__builtin_amdgcn_readlane((int)(my >> 32), b) << 32) |
+         (uint32_t)__builtin_amdgcn_readlane((int)my, b);
+  return b;
+}
 
 // q.k over one 16-byte chunk, fp32 accumulate.
 template <typename T>
@@ -166,13 +193,16 @@ __global__ __launch_bounds__((split_max_threads<T, D, GC, MASK>())) void decode_
   const int split = blockIdx.x;
   const int kvh = blockIdx.y / a.n_chunks;
   const int chunk = blockIdx.y - kvh * a.n_chunks;
-  const int b = blockIdx.z;
+  int64_t len_b = 0;
+  const int b = a.by_length
+                    ? length_ranked_batch(a.seq_lens, (int)gridDim.z, (int)blockIdx.z, lane, &len_b)
+                    : (int)blockIdx.z;
   const int h0 = kvh * a.group + chunk * a.chunk_heads;
   const int ng = min(a.chunk_heads, a.group - chunk * a.chunk_heads);
 
   int leff = a.kv_len;
   if (a.seq_lens != nullptr) {
-    const int64_t sl = a.seq_lens[b];
+    const int64_t sl = a.by_length ? len_b : a.seq_lens[b];
     leff = (int)(sl < 0 ? 0 : (sl < leff ? sl : leff));
   }
   // With per-sequence lengths the splits divide each sequence's own keys
@@ -803,7 +833,7 @@ int32_t check_common(const void* q, const void* k, const void* v,
 
 DecodeArgs fill_args(const void* q, const void* k, const void* v,
                      const uint8_t* mask, int64_t mask_sb, int64_t mask_sl,
-                     const int64_t* seq_lens, int64_t Hq, int64_t Hkv,
+                     const int64_t* seq_lens, int64_t B, int64_t Hq, int64_t Hkv,
                      int64_t L, int64_t S, int64_t q_sb, int64_t q_sh,
                      int64_t q_sd, int64_t k_sb, int64_t k_sh, int64_t k_sl,
                      int64_t v_sb, int64_t v_sh, int64_t v_sl, float sm_scale,
@@ -830,6 +860,7 @@ DecodeArgs fill_args(const void* q, const void* k, const void* v,
   const int64_t eb = dtype_bytes;
   a.q_vec = (q_sd == 1 && ((uintptr_t)q % 16) == 0 && ((q_sb * eb) % 16) == 0 &&
              ((q_sh * eb) % 16) == 0) ? 1 : 0;
+  a.by_length = (seq_lens != nullptr && mask == nullptr && B >= 2 && B <= 64) ? 1 : 0;
   return a;
 }
 
@@ -986,7 +1017,7 @@ extern "C" int32_t mi_decode_split(
     return MI_ERR_UNSUPPORTED;
   }
   Plan p = make_plan(dtype, batch, n_heads, n_kv_heads, kv_len, head_dim, num_splits);
-  DecodeArgs a = fill_args(q, k, v, mask, mask_sb, mask_sl, seq_lens, n_heads,
+  DecodeArgs a = fill_args(q, k, v, mask, mask_sb, mask_sl, seq_lens, batch, n_heads,
                            n_kv_heads, kv_len, num_splits, q_sb, q_sh, q_sd,
                            k_sb, k_sh, k_sl, v_sb, v_sh, v_sl, sm_scale, p,
                            elem_bytes(dtype));
@@ -1081,7 +1112,7 @@ extern "C" int32_t mi_flash_decode(
                             head_dim, 1, k_sl, v_sl, dtype);
   if (st != MI_OK) return st;
   Plan p = make_plan(dtype, batch, n_heads, n_kv_heads, kv_len, head_dim, 1);
-  DecodeArgs a = fill_args(q, k, v, mask, mask_sb, mask_sl, seq_lens, n_heads,
+  DecodeArgs a = fill_args(q, k, v, mask, mask_sb, mask_sl, seq_lens, batch, n_heads,
                            n_kv_heads, kv_len, 1, q_sb, q_sh, q_sd, k_sb, k_sh,
                            k_sl, v_sb, v_sh, v_sl, sm_scale, p, elem_bytes(dtype));
   a.out = out;
