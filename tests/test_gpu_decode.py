@@ -223,3 +223,34 @@ def test_mask_excluded_rows_are_not_read(dev, D, L, splits):
     empty = torch.isneginf(ref_lse)            # rows the mask empties entirely: -inf
     assert torch.equal(torch.isneginf(lse.cpu()), empty)
     assert max_abs(lse.cpu()[~empty], ref_lse[~empty]) < LSE_TOL
+
+
+@pytest.mark.parametrize("B", [2, 3, 64, 65])
+def test_seq_lens_rows_dealt_by_length(dev, B):
+    """With seq_lens and 2 <= B <= 64 the split kernel deals its grid rows by
+    sequence length (longest first, then shortest first); B = 65 keeps the
+    plain order.  Ties, empty sequences and lengths past the capacity
+    (clamped to it) must all land on their own rows: every row is checked
+    against the oracle, and a bit-identical rerun with the lengths permuted
+    with the batch shows the mapping is a permutation."""
+    T, Hq, Hkv, D = 320, 8, 2, 64
+    g = torch.Generator("cpu").manual_seed(B)
+    lens = torch.randint(0, T + 1, (B,), generator=g)
+    lens[0] = lens[-1]                       # a tie
+    lens[1] = 0                              # an empty sequence
+    if B > 2:
+        lens[2] = T + 50                     # past the capacity: clamped to T
+    q, k, v = _inputs(B, Hq, Hkv, T, D, torch.bfloat16, dev, seed=7)
+    out, lse = _fd()(q, k, v, seq_lens=lens.to(dev), num_splits=2, return_lse=True)
+    ref, ref_lse = ora.decode(q.cpu(), k.cpu(), v.cpu(), seq_lens=lens.clamp(max=T))
+    nonempty = lens > 0
+    assert max_abs(out[nonempty], ref[nonempty]) < TOL[torch.bfloat16]
+    assert max_abs(lse[nonempty], ref_lse[nonempty]) < LSE_TOL
+    assert torch.all(out[~nonempty] == 0)
+    assert torch.all(torch.isneginf(lse[~nonempty]))
+    perm = torch.randperm(B, generator=g)
+    pd = perm.to(dev)
+    out_p, lse_p = _fd()(q[pd].contiguous(), k[pd].contiguous(), v[pd].contiguous(),
+                         seq_lens=lens[perm].to(dev), num_splits=2, return_lse=True)
+    assert torch.equal(out_p, out[pd])
+    assert torch.equal(lse_p, lse[pd])
