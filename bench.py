@@ -249,10 +249,12 @@ def bench_config5(torch, steps: int, warmup: int) -> dict:
 
 def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
     """The seven W8A16 projections of one Llama-3.2-1B layer at config 2's token
-    count (M = 4 x 2048), one mi_w8a16_gemm call each, back to back."""
+    count (M = 4 x 2048), back to back, each through the model's GEMM dispatch
+    (w8a16_gemm_mfma: the split-K form where the tile grid leaves CUs idle)."""
     from src import _lib
+    from src.quant_linear import w8a16_gemm_mfma
     dev = torch.device("cuda:0")
-    lib = _lib.load()
+    _lib.load()
     M = 4 * 2048
     shapes = [("wq", 2048, 2048), ("wk", 512, 2048), ("wv", 512, 2048), ("wo", 2048, 2048),
               ("w1", 8192, 2048), ("w3", 8192, 2048), ("w2", 2048, 8192)]   # (name, N, K)
@@ -260,15 +262,10 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
     xs = {K: torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev) for K in (2048, 8192)}
     ws = [torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8).to(dev) for _, N, K in shapes]
     ss = [(torch.rand(N, generator=g) * 0.02 + 1e-3).to(torch.bfloat16).to(dev) for _, N, _ in shapes]
-    ys = [torch.empty(M, N, device=dev, dtype=torch.bfloat16) for _, N, _ in shapes]
-    stream = _lib.stream_of(xs[2048])
 
     def call(i):
         _, N, K = shapes[i]
-        x = xs[K]
-        st = lib.mi_w8a16_gemm(x.data_ptr(), ws[i].data_ptr(), ss[i].data_ptr(), ys[i].data_ptr(),
-                               M, N, K, K, K, 1, N, 0, 0, stream)
-        _lib.check(st, "w8a16_gemm")
+        w8a16_gemm_mfma(xs[K], ws[i], ss[i])
 
     def step():
         for i in range(len(shapes)):
@@ -303,7 +300,7 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
                         "achieved": dom["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(dom["tflops"] / BF16_PEAK_TFLOPS, 4),
                         "traffic": _traffic("w8a16_gemm_traffic.md", "hbm_bytes_per_launch_w1")}}
-    del xs, ws, ss, ys
+    del xs, ws, ss
     torch.cuda.empty_cache()
     return out
 

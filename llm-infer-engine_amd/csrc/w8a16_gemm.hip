@@ -448,16 +448,16 @@ extern "C" int32_t mi_w8a16_gemm(const void* x, const int8_t* w, const void* sca
 }
 
 // Split count for mi_w8a16_gemm_splitk (measured on MI355X): 1 (no split) once
-// the 128 x 256 tiles give half the CUs a workgroup (the partials' traffic and
-// the reduce launch then cost more than the longer per-workgroup chain);
-// otherwise about one workgroup per CU, each split at least 8 stages (512 k)
+// the 128 x 256 tiles give every CU a workgroup; otherwise about one workgroup
+// per CU (at one tile per two CUs the split still gains a little: wk / wv at
+// M = 8192, 37.0 -> 36.1 us), each split at least 8 stages (512 k)
 // deep, at most 8 splits, and the fp32 partials (written and read once) at
 // most 64 MiB.
 extern "C" int64_t mi_w8a16_gemm_splits(int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0 || k % kGmBK != 0) return 1;
   const int64_t tiles = ((m + kGmBM - 1) / kGmBM) * ((n + kGmBN - 1) / kGmBN);
   const int64_t cus = device_cu_count();
-  if (2 * tiles >= cus) return 1;
+  if (tiles >= cus) return 1;
   int64_t s = cus / tiles;
   const int64_t nk = k / kGmBK;
   if (s > nk / 8) s = nk / 8;
