@@ -221,13 +221,15 @@ def test_w8a16_gemm_splitk_c_side_validation(over, code, msg):
 
 
 def test_w8a16_gemm_split_rule():
-    """Splits only for grids under one 128 x 256 tile per two CUs (256 CUs
+    """Splits only for grids of fewer 128 x 256 tiles than CUs (256 CUs
     without a device): about one workgroup per CU, each split >= 8 stages,
     <= 8 splits, partials <= 64 MiB, and a count every split owns stages of."""
     from src import _lib
     lib = _lib.load()
     assert lib.mi_w8a16_gemm_splits(8192, 2048, 2048) == 1        # 512 tiles
-    assert lib.mi_w8a16_gemm_splits(2048, 2048, 2048) == 1        # 128 tiles: half the CUs
+    assert lib.mi_w8a16_gemm_splits(4096, 2048, 2048) == 1        # 256 tiles: every CU
+    assert lib.mi_w8a16_gemm_splits(2048, 2048, 2048) == 2        # 128 tiles: half the CUs
+    assert lib.mi_w8a16_gemm_splits(8192, 512, 2048) == 2         # wk / wv at M = 8192
     assert lib.mi_w8a16_gemm_splits(128, 2048, 2048) == 4         # 8 tiles, 32 stages
     assert lib.mi_w8a16_gemm_splits(512, 2048, 8192) == 8         # 32 tiles, 128 stages (K = 8192)
     assert lib.mi_w8a16_gemm_splits(128, 2048, 1024) == 2         # 16 stages -> 8 deep each
