@@ -54,6 +54,7 @@ struct GemmArgs {
   float* part;
   int32_t split_stages;
   int32_t part_vec;        // part rows allow 16-byte stores of 4 columns
+  int32_t y_line;          // y and its rows are 16-byte aligned (whole-line epilogue)
 };
 
 constexpr int kGmBM = 128;                      // output rows (m) per workgroup
@@ -279,6 +280,44 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
     return;
   }
   T* y = reinterpret_cast<T*>(a.y);
+  if (a.y_line && n0 + kGmBN <= a.N) {
+    // Whole-line stores: each wave stages its 64 columns of 32 rows at a time
+    // in LDS (the activation stages, free once every wave has read the last
+    // one) and writes each row's 128 bytes with 8 lanes x 16 bytes of one
+    // instruction, instead of 16-byte pieces of 32 rows from 8 instructions.
+    constexpr int RS = 136;                  // staged row stride (bytes, padded)
+    block_sync_lds();
+    unsigned char* const stg = smem_raw + wv * 32 * RS;
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    f32x4 s4[2][4];
+#pragma unroll
+    for (int nf = 0; nf < 2; ++nf)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        s4[nf][g] = *reinterpret_cast<const f32x4*>(sc_lds + 64 * wv + 32 * nf + 8 * g + 4 * h);
+#pragma unroll
+    for (int mf = 0; mf < 4; ++mf) {
+#pragma unroll
+      for (int nf = 0; nf < 2; ++nf)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          t4 v;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = Elem<T>::from_f32(acc[mf][nf][4 * g + i] * s4[nf][g][i]);
+          *reinterpret_cast<t4*>(stg + r * RS + (32 * nf + 8 * g + 4 * h) * 2) = v;
+        }
+      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's own rows are staged
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = 8 * i + (lane >> 3), cc = lane & 7;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * RS + cc * 16);
+        const int m = m0 + 32 * mf + rr;
+        if (m < a.M)
+          *reinterpret_cast<u32x4*>(y + (int64_t)m * a.y_sm + n0 + 64 * wv + 8 * cc) = v;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int nf = 0; nf < 2; ++nf) {
 #pragma unroll
@@ -382,7 +421,8 @@ int32_t gemm_setup(const char* what, const void* x, const int8_t* w, const void*
                scales, y, x_sm, w_sn, s_sn, y_sm, (int32_t)m, (int32_t)n, (int32_t)k,
                (int32_t)tiles_m, (int32_t)tiles_n,
                ((uintptr_t)y % 8 == 0 && y_sm % 4 == 0) ? 1 : 0,
-               nullptr, (int32_t)(k / kGmBK), 0};
+               nullptr, (int32_t)(k / kGmBK), 0,
+               ((uintptr_t)y % 16 == 0 && y_sm % 8 == 0) ? 1 : 0};
   return MI_OK;
 }
 
