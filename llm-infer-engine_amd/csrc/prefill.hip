@@ -62,6 +62,7 @@ struct PrefillArgs {
   const void* rsin;
   const int64_t* rpos;
   int64_t r_ss, r_rows;     // positions are clamped into the table's rows
+  int32_t o_line;           // out and its rows are 16-byte aligned (whole-row epilogue)
 };
 
 // RoPE of the Q fragments a lane holds for one 32-row block: chunk c (dims
@@ -847,6 +848,47 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
   for (; t < n_tiles; ++t) sync_tile(t);   // the block's remaining tiles
 
   if (n_tw == 0) return;
+  if (a.o_line) {
+    // Whole-row stores: each row block's 32 rows x 128 bytes are staged in a
+    // ring slot that no wave reads any more (every wave has passed the last
+    // tile barrier; only the last tile's slot is still read) and written back
+    // with 8 lanes x 16 bytes per row, one instruction per 8 rows.
+    constexpr int RS = 136;                  // staged row stride (bytes, padded)
+    unsigned char* const stg =
+        lds + ((n_tiles + (w >> 1)) % kSpBufs) * SLOT_B + (w & 1) * (32 * RS);
+    T* const ob = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_sb + (int64_t)head * a.o_sh;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      float lt = l[rb];
+      {  // both lane halves hold partial sums of the same row
+        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lt), __float_as_uint(lt), false, false);
+        lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      }
+      const float inv = 1.0f / lt;
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int d = 32 * db + 8 * q4 + 4 * hh;
+          const uint32_t w0 = MM::pack2(o[rb][db][4 * q4] * inv, o[rb][db][4 * q4 + 1] * inv);
+          const uint32_t w1 = MM::pack2(o[rb][db][4 * q4 + 2] * inv, o[rb][db][4 * q4 + 3] * inv);
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<u32x2*>(stg + lr * RS + d * 2) = u32x2{w0, w1};
+        }
+      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's rows are staged
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rr = 8 * i + (lane >> 3), cc = lane & 7;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * RS + cc * 16);
+        const int qr = r0 + 32 * rb + rr;
+        if (qr < a.S) *reinterpret_cast<u32x4*>(ob + (int64_t)qr * a.o_ss + 8 * cc) = v;
+      }
+      const int qrow = r0 + 32 * rb + lr;
+      if (a.lse != nullptr && hh == 0 && qrow < a.S)
+        a.lse[((int64_t)b * a.Hq + head) * a.S + qrow] = (m[rb] + __log2f(lt)) * kLn2;
+    }
+    return;
+  }
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
     float lt = l[rb];
@@ -1099,6 +1141,7 @@ int32_t attn_prefill(const void* q, const void* k, const void* v, void* o, float
   a.scale_log2 = sm_scale * kLog2e;
   a.rcos = rq.cos; a.rsin = rq.sin; a.rpos = rq.pos;
   a.r_ss = rq.row_stride; a.r_rows = rq.rows;
+  a.o_line = (po % 16 == 0 && ((o_sb | o_sh | o_ss) * eb) % 16 == 0) ? 1 : 0;
   const int nwaves = gh * pj;
   const int64_t blocks = (int64_t)a.B * a.Hkv * a.head_chunks * a.n_pb;
   if (blocks > INT32_MAX) {
