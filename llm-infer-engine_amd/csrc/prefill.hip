@@ -429,6 +429,47 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
   }
 
   if (!wave_active) return;
+  if (a.o_line) {
+    // Whole-row stores: every wave has passed the last tile's barrier, so the
+    // tile buffers are free; each wave stages its 32 rows at a time there and
+    // writes a row's 2*D bytes with D/8 lanes x 16 bytes of one instruction.
+    constexpr int RS = 2 * D + 8;            // staged row stride (bytes, padded)
+    constexpr int LPRO = D / 8, RPI = 64 / LPRO;
+    static_assert(4 * 32 * RS <= 2 * 2 * 64 * D * (int)sizeof(T), "staging fits the tile buffers");
+    unsigned char* const stg = lds + w * 32 * RS;
+    T* const ob = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_sb + (int64_t)head * a.o_sh;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float lt = l[rb];
+      {  // both lane halves hold partial sums of the same row
+        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lt), __float_as_uint(lt), false, false);
+        lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+      }
+      const float inv = 1.0f / lt;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int d = 32 * db + 8 * q4 + 4 * hh;
+          const uint32_t w0 = MM::pack2(o[rb][db][4 * q4] * inv, o[rb][db][4 * q4 + 1] * inv);
+          const uint32_t w1 = MM::pack2(o[rb][db][4 * q4 + 2] * inv, o[rb][db][4 * q4 + 3] * inv);
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          *reinterpret_cast<u32x2*>(stg + lr * RS + d * 2) = u32x2{w0, w1};
+        }
+      __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // this wave's rows are staged
+#pragma unroll
+      for (int i = 0; i < 32 / RPI; ++i) {
+        const int rr = RPI * i + lane / LPRO, cc = lane % LPRO;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * RS + cc * 16);
+        const int qr = qpos0 + 32 * rb + rr;
+        if (qr < a.S) *reinterpret_cast<u32x4*>(ob + (int64_t)qr * a.o_ss + 8 * cc) = v;
+      }
+      const int qrow = qpos0 + 32 * rb + lr;
+      if (a.lse != nullptr && hh == 0 && qrow < a.S)
+        a.lse[((int64_t)b * a.Hq + head) * a.S + qrow] = (m[rb] + __log2f(lt)) * kLn2;
+    }
+    return;
+  }
 #pragma unroll
   for (int rb = 0; rb < RB; ++rb) {
     float lt = l[rb];
