@@ -563,6 +563,7 @@ __global__ __launch_bounds__(256) void decode_combine_wave_kernel(CombineArgs a)
     acc[i] = x;
   }
   if (sg == 0) {
+    T ov[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float o;
@@ -570,9 +571,16 @@ __global__ __launch_bounds__(256) void decode_combine_wave_kernel(CombineArgs a)
         o = acc[i] / fmaxf(den, 1.0f);
       else
         o = a.empty_nan ? __builtin_nanf("") : 0.f;
-      T* op = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
-              (int64_t)(4 * c + i) * a.o_sd;
-      *op = Elem<T>::from_f32(o);
+      ov[i] = Elem<T>::from_f32(o);
+    }
+    T* op = reinterpret_cast<T*>(a.out) + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh +
+            (int64_t)(4 * c) * a.o_sd;
+    if (a.o_sd == 1 && ((uintptr_t)op % (4 * sizeof(T))) == 0) {   // the 4 columns in one store
+      typedef T t4 __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<t4*>(op) = t4{ov[0], ov[1], ov[2], ov[3]};
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) op[(int64_t)i * a.o_sd] = ov[i];
     }
   }
   if (lane == 0 && a.lse != nullptr)
