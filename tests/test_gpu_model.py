@@ -62,8 +62,8 @@ def test_prefill_then_decode_matches_oracle(dev, quantized):
         ref = omodel.decode_step(model, tok, pos, ck, cv, args.norm_eps)
         _logit_check(logits, ref)
         # the new slot of every layer holds RoPE(K) / V of this token (bf16)
-        assert max_abs(kv.k[:, :B, :, pos], ck[:, :B, :, pos]) < 3e-2 * float(ck[:, :B, :, pos].abs().max())
-        assert max_abs(kv.v[:, :B, :, pos], cv[:, :B, :, pos]) < 3e-2 * float(cv[:, :B, :, pos].abs().max())
+        assert max_abs(kv.k[:, :B, :, pos], ck[:, :B, :, pos]) < 2e-2 * float(ck[:, :B, :, pos].abs().max())
+        assert max_abs(kv.v[:, :B, :, pos], cv[:, :B, :, pos]) < 2e-2 * float(cv[:, :B, :, pos].abs().max())
         pos += 1
 
 
@@ -94,8 +94,8 @@ def test_graph_runner_matches_eager(dev):
         # layer 0 sees identical inputs -> identical slots; deeper layers may
         # differ in the last bits (decode work split differs between the two)
         assert torch.equal(kv.k[0], graph_k[0]) and torch.equal(kv.v[0], graph_v[0])
-        assert max_abs(kv.k, graph_k) < 3e-2 * float(graph_k.abs().max())
-        assert max_abs(kv.v, graph_v) < 3e-2 * float(graph_v.abs().max())
+        assert max_abs(kv.k, graph_k) < 2e-2 * float(graph_k.abs().max())
+        assert max_abs(kv.v, graph_v) < 2e-2 * float(graph_v.abs().max())
         _logit_check(g_logits, e_logits)
         pos += 1
     with pytest.raises(ValueError, match="out of range"):
