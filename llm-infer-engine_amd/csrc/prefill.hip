@@ -27,7 +27,10 @@
 //    src/flash_attn.py:63,72).
 //  * head_dim 64: a software-pipelined kernel (each wave overlaps its own
 //    MFMAs with its softmax, 4-slot LDS ring, one barrier per tile);
-//    head_dim 128: double-buffered tiles, one barrier per tile.
+//    head_dim 32 / 128: double-buffered tiles, one barrier per tile.
+//  * The prologue issues the first tile copies before the Q loads (one memory
+//    round trip for both); the epilogue stages the output rows in the freed
+//    LDS and writes whole 2*D-byte rows with 16-byte lanes.
 //  * Blocks are ordered heaviest-first (longest causal prefix) and mapped so
 //    that all blocks of one (batch, kv-head) land on the same XCD, whose L2
 //    then serves the K/V re-reads.
