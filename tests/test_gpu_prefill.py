@@ -184,3 +184,31 @@ def test_fused_q_rope_fp32_and_mixed_tables(dev):
         assert torch.equal(a, b)
     with pytest.raises(ValueError, match="rows"):
         _fa()(q, k, v, rope_cos=cos[:10], rope_sin=sin[:10])
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_epilogue_store_paths_agree(dev, D):
+    """The kernels write 16-byte-aligned output rows through an LDS-staged
+    whole-row epilogue and other rows with 8-byte stores: an output buffer
+    offset by 8 bytes (rows 8- but not 16-byte aligned) takes the second
+    path and must hold the same bits."""
+    from src import _lib
+    B, Hq, Hkv, S = 2, 8, 2, 333
+    q = randn((B, Hq, S, D), 11, torch.bfloat16, dev)
+    k = randn((B, Hkv, S, D), 12, torch.bfloat16, dev)
+    v = randn((B, Hkv, S, D), 13, torch.bfloat16, dev)
+    out, lse = _fa()(q, k, v, return_lse=True)
+    buf = torch.full((B * Hq * S * D + 8,), 5.0, device=dev, dtype=torch.bfloat16)
+    o = buf[4:4 + B * Hq * S * D].view(B, Hq, S, D)
+    assert o.data_ptr() % 16 == 8
+    lse2 = torch.empty_like(lse)
+    lib = _lib.load()
+    st = lib.mi_attn_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+                             lse2.data_ptr(), B, Hq, Hkv, S, S, D,
+                             *q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *o.stride()[:3],
+                             1.0 / D ** 0.5, _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    _lib.check(st, "mi_attn_prefill")
+    torch.cuda.synchronize()
+    assert torch.equal(o, out)
+    assert torch.equal(lse2, lse)
+    assert torch.all(buf[:4] == 5.0) and torch.all(buf[4 + B * Hq * S * D:] == 5.0)

@@ -170,3 +170,25 @@ def test_split_k_default_rule_and_strided_output(dev):
     _lib.check(st, "w8a16_gemm_splitk")
     assert _rel(y[:, :N], oq.w8a16(x, q, s)) < 2e-2
     assert torch.all(y[:, N:] == 3.0)
+
+
+def test_epilogue_store_paths_agree(dev):
+    """16-byte-aligned y rows take the LDS-staged whole-line epilogue, rows
+    only 8-byte aligned (row stride 1028) the 8-byte stores: same bits."""
+    from src import _lib
+    M, K, N = 300, 512, 1024
+    q, s = _quantised(N, K, torch.bfloat16, dev, 9)
+    x = _x(M, K, torch.bfloat16, dev, 10)
+    lib = _lib.load()
+    ys = []
+    for stride in (N, N + 4):
+        y = torch.full((M, stride), 3.0, device=dev, dtype=torch.bfloat16)
+        st = lib.mi_w8a16_gemm(x.data_ptr(), q.data_ptr(), s.data_ptr(), y.data_ptr(), M, N, K,
+                               x.stride(0), q.stride(0), s.stride(0), y.stride(0),
+                               _lib.dtype_code(x.dtype), _lib.dtype_code(s.dtype), _lib.stream_of(x))
+        _lib.check(st, "w8a16_gemm")
+        ys.append(y)
+    assert (N + 4) * 2 % 16 == 8
+    assert torch.equal(ys[0], ys[1][:, :N])
+    assert torch.all(ys[1][:, N:] == 3.0)
+    assert _rel(ys[0], oq.w8a16(x, q, s)) < 2e-2
