@@ -808,8 +808,8 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
     constexpr bool HAS_PV = decltype(has_pv_c)::value, DIAG = decltype(diag_c)::value;
     if constexpr (HAS_PV) pv(prv, 1, pB, TT{});
     qk(cur, 1, sB, std::integral_constant<bool, !DIAG>{});
-    if constexpr (!HAS_PV) {  // the wave's first tile: no running max yet
-      if (smax(sA, pA, TT{}, std::integral_constant<bool, DIAG>{}, FF{})) rescale_o(TT{});
+    if constexpr (!HAS_PV) {  // the wave's first tile: no running max yet, O still zero
+      smax(sA, pA, TT{}, std::integral_constant<bool, DIAG>{}, FF{});
     } else {
       const bool fb = smax_fast(sA, pA, TT{}, std::integral_constant<bool, DIAG>{}, FF{});
       if constexpr (!DIAG) interleave();
