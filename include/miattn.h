@@ -162,11 +162,15 @@ int64_t mi_decode_default_splits(int64_t batch, int64_t n_heads,
  * Rotate-half RoPE of x [batch, n_heads, seq_len, head_dim] into out (any
  * strides).  Row s uses cos/sin row s of the [seq_len, head_dim/2] tables
  * (the caller slices the table at start_pos), or row positions[s] when
- * positions (device int64 [seq_len]) is not NULL.  cdtype is the table dtype.
+ * positions (device int64 [seq_len]) is not NULL.  table_rows is the number of
+ * cos/sin rows (>= seq_len without positions; a position outside
+ * [0, table_rows) uses the nearest row, as the fused prefill and decode RoPE
+ * do).  cdtype is the table dtype.
  * Replaces rope_kernel + apply_rotary  src/rope.py:48-91, src/rope.py:94-119.
  */
 int32_t mi_rope(const void* x, void* out, const void* cos, const void* sin,
-                const int64_t* positions, int64_t batch, int64_t n_heads, int64_t seq_len,
+                const int64_t* positions, int64_t table_rows, int64_t batch,
+                int64_t n_heads, int64_t seq_len,
                 int64_t head_dim, int64_t x_sb, int64_t x_sh, int64_t x_ss,
                 int64_t x_sd, int64_t o_sb, int64_t o_sh, int64_t o_ss,
                 int64_t o_sd, int64_t c_ss, int64_t c_sd, int64_t s_ss,
@@ -179,15 +183,18 @@ int32_t mi_rope(const void* x, void* out, const void* cos, const void* sin,
  * token shared by the batch) when positions != NULL.  cache_k/cache_v point
  * at the layer view [batch, n_kv_heads, capacity, head_dim]; slots outside
  * [0, capacity) are never written.  cos/sin rows are indexed by s, or by pos
- * when cos_by_position != 0 (device-resident full table).  With cos = sin =
- * NULL, K is copied unrotated (plain cache write, KVCache.update).
+ * when cos_by_position != 0 (device-resident full table; a slot past its
+ * table_rows rows uses the last row).  table_rows >= seq_len otherwise.  With
+ * cos = sin = NULL, K is copied unrotated (plain cache write, KVCache.update)
+ * and table_rows is ignored.
  * Replaces _rope_k_cache_write_seq_kernel / _scatter_kernel +
  * rope_and_cache_update  src/rope.py:122-252, src/rope.py:255-313.
  */
 int32_t mi_rope_kv_append(const void* xk, const void* xv, const void* cos,
                           const void* sin, void* cache_k, void* cache_v,
                           int64_t start_pos, const int64_t* positions,
-                          int64_t batch, int64_t n_kv_heads, int64_t seq_len,
+                          int64_t table_rows, int64_t batch,
+                          int64_t n_kv_heads, int64_t seq_len,
                           int64_t head_dim, int64_t capacity, int64_t xk_sb,
                           int64_t xk_sh, int64_t xk_ss, int64_t xk_sd,
                           int64_t xv_sb, int64_t xv_sh, int64_t xv_ss,

@@ -24,6 +24,7 @@ struct RopeArgs {
   const void* cos;
   const void* sin;
   const int64_t* positions;  // null: table row s; else row positions[s]
+  int64_t rows;              // table rows: positions are clamped into [0, rows)
   int64_t x_sb, x_sh, x_ss, x_sd;
   int64_t o_sb, o_sh, o_ss, o_sd;
   int64_t c_ss, c_sd, s_ss, s_sd;
@@ -42,7 +43,8 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     const int b = (int)(r / a.H);
     const T* xp = reinterpret_cast<const T*>(a.x) + b * a.x_sb + h * a.x_sh + s * a.x_ss;
     T* op = reinterpret_cast<T*>(a.out) + b * a.o_sb + h * a.o_sh + s * a.o_ss;
-    const int64_t crow = a.positions != nullptr ? a.positions[s] : s;
+    const int64_t crow =
+        a.positions != nullptr ? min(max(a.positions[s], (int64_t)0), a.rows - 1) : s;
     const CT* cp = reinterpret_cast<const CT*>(a.cos) + crow * a.c_ss + i * a.c_sd;
     const CT* sp = reinterpret_cast<const CT*>(a.sin) + crow * a.s_ss + i * a.s_sd;
     const float x1 = Elem<T>::to_f32(xp[i * a.x_sd]);
@@ -69,6 +71,7 @@ struct KvAppendArgs {
   int64_t cv_sb, cv_sh, cv_st, cv_sd;
   int64_t c_ss, c_sd, s_ss, s_sd;
   int64_t capacity;  // T: slots outside [0, T) are never written
+  int64_t rows;      // table rows: a position past them uses the last row
   int32_t B, H, S, half;
   int32_t cos_by_pos;  // cos/sin rows indexed by absolute position, not s
 };
@@ -85,7 +88,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(KvAppendArgs a) {
     const int b = (int)(r / a.H);
     const int64_t pos = a.positions != nullptr ? a.positions[s] : a.start_pos + s;
     if (pos < 0 || pos >= a.capacity) continue;
-    const int64_t crow = a.cos_by_pos ? pos : s;
+    const int64_t crow = a.cos_by_pos ? min(pos, a.rows - 1) : s;
     const T* kp = reinterpret_cast<const T*>(a.xk) + b * a.xk_sb + h * a.xk_sh + s * a.xk_ss;
     const T* vp = reinterpret_cast<const T*>(a.xv) + b * a.xv_sb + h * a.xv_sh + s * a.xv_ss;
     T* kc = reinterpret_cast<T*>(a.ck) + b * a.ck_sb + h * a.ck_sh + pos * a.ck_st;
@@ -143,7 +146,8 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a) {
       const int s = (int)(t / nj), i0 = 8 * (int)(t % nj);
       const T* xp = reinterpret_cast<const T*>(a.x) + b * a.x_sb + h * a.x_sh + s * a.x_ss + i0;
       T* op = reinterpret_cast<T*>(a.out) + b * a.o_sb + h * a.o_sh + s * a.o_ss + i0;
-      const int64_t crow = a.positions != nullptr ? a.positions[s] : s;
+      const int64_t crow =
+          a.positions != nullptr ? min(max(a.positions[s], (int64_t)0), a.rows - 1) : s;
       const T* cp = reinterpret_cast<const T*>(a.cos) + crow * a.c_ss + i0;
       const T* sp = reinterpret_cast<const T*>(a.sin) + crow * a.s_ss + i0;
       u32x4 ya, yb;
@@ -171,7 +175,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_vec_kernel(KvAppendArgs a)
       const u32x4 k1 = load16(kp), k2 = load16(kp + a.half);
       const u32x4 v1 = load16(vp), v2 = load16(vp + a.half);
       if (a.cos != nullptr) {
-        const int64_t crow = a.cos_by_pos ? pos : s;
+        const int64_t crow = a.cos_by_pos ? min(pos, a.rows - 1) : s;
         const T* cp = reinterpret_cast<const T*>(a.cos) + crow * a.c_ss + i0;
         const T* sp = reinterpret_cast<const T*>(a.sin) + crow * a.s_ss + i0;
         u32x4 ya, yb;
@@ -257,7 +261,7 @@ using namespace mi;
 
 extern "C" int32_t mi_rope(const void* x, void* out, const void* cos,
                            const void* sin, const int64_t* positions,
-                           int64_t batch, int64_t n_heads,
+                           int64_t table_rows, int64_t batch, int64_t n_heads,
                            int64_t seq_len, int64_t head_dim, int64_t x_sb,
                            int64_t x_sh, int64_t x_ss, int64_t x_sd,
                            int64_t o_sb, int64_t o_sh, int64_t o_ss,
@@ -278,8 +282,14 @@ extern "C" int32_t mi_rope(const void* x, void* out, const void* cos,
   }
   const int64_t total = batch * n_heads * seq_len * (head_dim / 2);
   if (total == 0) return MI_OK;
+  if (table_rows < (positions != nullptr ? 1 : seq_len)) {
+    set_last_error("rope: cos/sin have %lld rows, need %lld", (long long)table_rows,
+                   (long long)(positions != nullptr ? 1 : seq_len));
+    return MI_ERR_INVALID;
+  }
   RopeArgs a{};
   a.x = x; a.out = out; a.cos = cos; a.sin = sin; a.positions = positions;
+  a.rows = table_rows;
   a.x_sb = x_sb; a.x_sh = x_sh; a.x_ss = x_ss; a.x_sd = x_sd;
   a.o_sb = o_sb; a.o_sh = o_sh; a.o_ss = o_ss; a.o_sd = o_sd;
   a.c_ss = c_ss; a.c_sd = c_sd; a.s_ss = s_ss; a.s_sd = s_sd;
@@ -306,7 +316,7 @@ extern "C" int32_t mi_rope(const void* x, void* out, const void* cos,
 extern "C" int32_t mi_rope_kv_append(
     const void* xk, const void* xv, const void* cos, const void* sin,
     void* cache_k, void* cache_v, int64_t start_pos, const int64_t* positions,
-    int64_t batch, int64_t n_kv_heads, int64_t seq_len, int64_t head_dim,
+    int64_t table_rows, int64_t batch, int64_t n_kv_heads, int64_t seq_len, int64_t head_dim,
     int64_t capacity, int64_t xk_sb, int64_t xk_sh, int64_t xk_ss,
     int64_t xk_sd, int64_t xv_sb, int64_t xv_sh, int64_t xv_ss, int64_t xv_sd,
     int64_t ck_sb, int64_t ck_sh, int64_t ck_st, int64_t ck_sd, int64_t cv_sb,
@@ -335,6 +345,11 @@ extern "C" int32_t mi_rope_kv_append(
   }
   const int64_t total = batch * n_kv_heads * seq_len * (head_dim / 2);
   if (total == 0) return MI_OK;
+  if (cos != nullptr && table_rows < (cos_by_position ? 1 : seq_len)) {
+    set_last_error("rope_kv_append: cos/sin have %lld rows, need %lld", (long long)table_rows,
+                   (long long)(cos_by_position ? 1 : seq_len));
+    return MI_ERR_INVALID;
+  }
   KvAppendArgs a{};
   a.xk = xk; a.xv = xv; a.cos = cos; a.sin = sin; a.ck = cache_k; a.cv = cache_v;
   a.positions = positions;
@@ -345,6 +360,7 @@ extern "C" int32_t mi_rope_kv_append(
   a.cv_sb = cv_sb; a.cv_sh = cv_sh; a.cv_st = cv_st; a.cv_sd = cv_sd;
   a.c_ss = c_ss; a.c_sd = c_sd; a.s_ss = s_ss; a.s_sd = s_sd;
   a.capacity = capacity;
+  a.rows = table_rows;
   a.B = (int32_t)batch; a.H = (int32_t)n_kv_heads; a.S = (int32_t)seq_len;
   a.half = (int32_t)(head_dim / 2);
   a.cos_by_pos = cos_by_position;

@@ -104,6 +104,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ]),
     "mi_rope": (_i32, [
         _ptr, _ptr, _ptr, _ptr, _ptr,          # x out cos sin positions
+        _i64,                                  # table_rows
         _i64, _i64, _i64, _i64,
         _i64, _i64, _i64, _i64,
         _i64, _i64, _i64, _i64,
@@ -112,7 +113,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ]),
     "mi_rope_kv_append": (_i32, [
         _ptr, _ptr, _ptr, _ptr, _ptr, _ptr,    # xk xv cos sin cache_k cache_v
-        _i64, _ptr,                            # start_pos positions
+        _i64, _ptr, _i64,                      # start_pos positions table_rows
         _i64, _i64, _i64, _i64, _i64,          # B Hkv S D capacity
         _i64, _i64, _i64, _i64,                # xk strides
         _i64, _i64, _i64, _i64,                # xv strides

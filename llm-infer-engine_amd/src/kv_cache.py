@@ -53,7 +53,7 @@ class KVCache:
         code = _lib.dtype_code(self.dtype)
         st = lib.mi_rope_kv_append(
             k_val.data_ptr(), v_val.data_ptr(), None, None,
-            ck.data_ptr(), cv.data_ptr(), int(start_pos), _lib.ptr(positions),
+            ck.data_ptr(), cv.data_ptr(), int(start_pos), _lib.ptr(positions), 0,
             B, H, S, D, self.max_seq_len,
             *k_val.stride(), *v_val.stride(), *ck.stride(), *cv.stride(),
             0, 0, 0, 0, 0, code, code, _lib.stream_of(ck))

@@ -82,18 +82,18 @@ def apply_rotary(x, cos, sin, *, positions=None):
     """Rotate-half RoPE of x [B, n_heads, seq_len, head_dim] with cos/sin
     [seq_len, head_dim // 2]; returns a new tensor with x's strides
     (src/rope.py:94-119).  ``positions`` (keyword-only extension, device int64
-    [seq_len]): cos/sin are full tables and token s uses row positions[s]."""
+    [seq_len]): cos/sin are full tables and token s uses row positions[s]
+    (clamped into the table's rows)."""
     B, n_heads, seq_len, head_dim = x.shape
     _lib.require_device(x, "apply_rotary")
-    if positions is None:
-        _check_tables(cos, sin, seq_len, head_dim, "apply_rotary")
-    elif positions.dtype != torch.int64 or positions.device != x.device:
+    _check_tables(cos, sin, seq_len if positions is None else 1, head_dim, "apply_rotary")
+    if positions is not None and (positions.dtype != torch.int64 or positions.device != x.device):
         positions = positions.to(device=x.device, dtype=torch.int64)
     out = torch.empty_like(x)
     lib = _lib.load()
     st = lib.mi_rope(
         x.data_ptr(), out.data_ptr(), cos.data_ptr(), sin.data_ptr(), _lib.ptr(positions),
-        B, n_heads, seq_len, head_dim,
+        min(cos.shape[0], sin.shape[0]), B, n_heads, seq_len, head_dim,
         *x.stride(), *out.stride(), *cos.stride(), *sin.stride(),
         _lib.dtype_code(x.dtype), _lib.dtype_code(cos.dtype), _lib.stream_of(x))
     _lib.check(st, "apply_rotary")
@@ -126,8 +126,8 @@ def rope_and_cache_update(xk, xv, rope_cos, rope_sin, kv_cache, layer_idx,
     _lib.require_device(xk, "rope_and_cache_update")
     if scatter_positions is None and start_pos is None:
         raise ValueError("rope_and_cache_update needs start_pos or scatter_positions")
-    if not cos_by_position:
-        _check_tables(rope_cos, rope_sin, input_len, head_dim, "rope_and_cache_update")
+    _check_tables(rope_cos, rope_sin, 1 if cos_by_position else input_len, head_dim,
+                  "rope_and_cache_update")
     cache_k = kv_cache.k[layer_idx, :B]
     cache_v = kv_cache.v[layer_idx, :B]
     if xk.dtype != cache_k.dtype or xv.dtype != cache_v.dtype:
@@ -144,7 +144,7 @@ def rope_and_cache_update(xk, xv, rope_cos, rope_sin, kv_cache, layer_idx,
         xk.data_ptr(), xv.data_ptr(), rope_cos.data_ptr(), rope_sin.data_ptr(),
         cache_k.data_ptr(), cache_v.data_ptr(),
         0 if start_pos is None else int(start_pos), _lib.ptr(positions),
-        B, n_kv_heads, input_len, head_dim, cache_k.shape[2],
+        min(rope_cos.shape[0], rope_sin.shape[0]), B, n_kv_heads, input_len, head_dim, cache_k.shape[2],
         *xk.stride(), *xv.stride(), *cache_k.stride(), *cache_v.stride(),
         *rope_cos.stride(), *rope_sin.stride(), int(bool(cos_by_position)),
         _lib.dtype_code(xk.dtype), _lib.dtype_code(rope_cos.dtype), _lib.stream_of(xk))

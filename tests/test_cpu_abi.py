@@ -83,9 +83,24 @@ def test_rope_kv_append_rejects_out_of_capacity():
     from src import _lib
     lib = _lib.load()
     st = lib.mi_rope_kv_append(1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20,
-                               60, None, 1, 8, 10, 64, 64,
+                               60, None, 64, 1, 8, 10, 64, 64,
                                *([1] * 16), 1, 1, 1, 1, 0, 0, 0, None)
     assert st == -1 and "capacity" in _lib.last_error()
+
+
+@pytest.mark.parametrize("positions,rows", [(None, 9), (1 << 26, 0)])
+def test_rope_table_rows_checked_before_launch(positions, rows):
+    """Without positions the tables need seq_len (10) rows; with device
+    positions (clamped into the table in the kernel) at least one."""
+    from src import _lib
+    lib = _lib.load()
+    st = lib.mi_rope(1 << 20, 1 << 21, 1 << 22, 1 << 23, positions, rows, 1, 8, 10, 64,
+                     *([1] * 16), 0, 0, None)
+    assert st == -1 and "rows" in _lib.last_error()
+    st = lib.mi_rope_kv_append(1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20, 1 << 20,
+                               0, positions, rows, 1, 8, 10, 64, 64,
+                               *([1] * 16), 1, 1, 1, 1, int(positions is not None), 0, 0, None)
+    assert st == -1 and "rows" in _lib.last_error()
 
 
 def _prefill_rope_call(lib, **over):

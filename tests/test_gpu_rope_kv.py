@@ -156,3 +156,29 @@ def test_rope_and_cache_update_fp16_and_unaligned_fallback(dev):
                                             cos[start:start + S], sin[start:start + S],
                                             start_pos=start)
         assert torch.equal(kv.k.cpu(), ref_k) and torch.equal(kv.v.cpu(), ref_v)
+
+
+@pytest.mark.parametrize("dtype,tdtype", [(torch.bfloat16, torch.bfloat16),
+                                          (torch.bfloat16, torch.float32)])
+def test_positions_outside_the_table_use_the_nearest_row(dev, dtype, tdtype):
+    """Device positions are not checked on the host (that would need a sync):
+    a position outside the table's rows reads the nearest row, never past
+    the table, for Q RoPE and for the cache append by absolute position."""
+    from src.rope import apply_rotary, rope_and_cache_update
+    B, H, D, T = 2, 4, 64, 48
+    pos = torch.tensor([-5, 0, 47, 48, 1000], dtype=torch.int64, device=dev)
+    clamped = pos.clamp(0, T - 1)
+    _, cos, sin = _tables(D, T, tdtype, dev)
+    x = randn((B, H, pos.numel(), D), 90, dtype, dev)
+    out = apply_rotary(x, cos, sin, positions=pos)
+    assert torch.equal(out.cpu(), orope.rotate(x, cos.cpu()[clamped.cpu()], sin.cpu()[clamped.cpu()]))
+    # cache append: slots 40..55 of a 64-slot cache, table rows 0..47
+    kv = _cache(1, B, H, 64, D, dtype, dev)
+    slots = torch.arange(40, 56, device=dev)
+    xk = randn((B, H, slots.numel(), D), 91, dtype, dev)
+    xv = randn((B, H, slots.numel(), D), 92, dtype, dev)
+    rope_and_cache_update(xk, xv, cos, sin, kv, 0, scatter_positions=slots, cos_by_position=True)
+    rows = slots.clamp(max=T - 1).cpu()
+    ref_k = orope.rotate(xk, cos.cpu()[rows], sin.cpu()[rows])
+    assert torch.equal(kv.k[0, :, :, 40:56].cpu(), ref_k)
+    assert torch.equal(kv.v[0, :, :, 40:56].cpu(), xv.cpu())
