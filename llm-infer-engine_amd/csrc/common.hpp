@@ -93,14 +93,16 @@ __device__ inline float dpp_f32(float x) {
       __builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
-// Sum over aligned groups of N lanes (N in {1,2,4,8,16}); every lane of the
-// group receives the total.  Uses only intra-row DPP (no LDS traffic).
+// Sum over aligned groups of N lanes (N in {1,2,4,8,16,32}); every lane of the
+// group receives the total.  Up to 16 lanes intra-row DPP only (no LDS
+// traffic); 32 adds one exchange between neighbouring rows.
 template <int N>
 __device__ inline float group_sum(float x) {
   if constexpr (N >= 2) x += dpp_f32<0xB1>(x);   // quad_perm [1,0,3,2]
   if constexpr (N >= 4) x += dpp_f32<0x4E>(x);   // quad_perm [2,3,0,1]
   if constexpr (N >= 8) x += dpp_f32<0x141>(x);  // row_half_mirror
   if constexpr (N >= 16) x += dpp_f32<0x140>(x); // row_mirror
+  if constexpr (N >= 32) x += __shfl_xor(x, 16, 64);
   return x;
 }
 

@@ -960,19 +960,22 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
   }
 }
 
-// fp32 inputs: plain VALU flash attention (no fp32 MFMA tiles).  TPR = D/8
-// lanes per query row, 8 dims each (32 rows per 256-thread block at D = 64,
-// 16 at D = 128, so a short sequence still gives the GPU hundreds of blocks
-// and a long row's chain of keys is split over many lanes); K/V tiles staged
-// in LDS with 16-byte copies and read back as 16-byte broadcasts.  Keys are
-// taken 8 at a time: 8 independent dot-product chains, one running-max update
-// and one rescale per group of 8.  Optional q RoPE in the prologue (the RoPE
-// kernels' rounding).  Used for fp32 models (e.g. the CPU-shaped parity case).
-template <int D>
-__global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillArgs a) {
+// Plain VALU flash attention in fp32 arithmetic: every head dim of fp32
+// inputs (no fp32 MFMA tiles), and head dims 16 and 256 of bf16/fp16 inputs
+// (the MFMA kernels cover 32, 64 and 128).  TPR = D/8 lanes per query row, 8
+// dims each (32 rows per 256-thread block at D = 64, 16 at D = 128, so a short
+// sequence still gives the GPU hundreds of blocks and a long row's chain of
+// keys is split over many lanes); K/V tiles converted to fp32 and staged in
+// LDS with 16-byte copies, read back as 16-byte broadcasts.  Keys are taken 8
+// at a time: 8 independent dot-product chains, one running-max update and one
+// rescale per group of 8.  Optional q RoPE in the prologue (the RoPE kernels'
+// rounding to T).  Outputs are rounded once to T.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prefill_valu_kernel(PrefillArgs a) {
   constexpr int DL = 8, TPR = D / DL, BN = 4096 / D;  // K+V tiles: 32 KB of LDS
   constexpr int ROWS = 256 / TPR;  // query rows per block
   constexpr int KB = 8;            // keys per softmax update
+  constexpr int CN = Chunk<T>::kN; // elements per 16-byte chunk
   __shared__ __align__(16) float ks[BN][D];
   __shared__ __align__(16) float vs[BN][D];
   typedef float f4 __attribute__((ext_vector_type(4)));
@@ -985,38 +988,44 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillArgs a) {
   const int kvh = head / a.G;
   const int qrow = rb * ROWS + row_in;
   const int qr = min(qrow, a.S - 1);
-  const float* qp = reinterpret_cast<const float*>(a.q) + (int64_t)b * a.q_sb +
-                    (int64_t)head * a.q_sh + (int64_t)qr * a.q_ss;
+  const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                (int64_t)head * a.q_sh + (int64_t)qr * a.q_ss;
   float qv[DL], acc[DL];
 #pragma unroll
-  for (int i = 0; i < DL; ++i) { qv[i] = qp[part * DL + i]; acc[i] = 0.f; }
+  for (int i = 0; i < DL; ++i) { qv[i] = Elem<T>::to_f32(qp[part * DL + i]); acc[i] = 0.f; }
   if (a.rcos != nullptr) {
     // rotation partner of dim d is d + D/2 (or d - D/2): lane part +- TPR/2
     int64_t crow = qr;
     if (a.rpos != nullptr) crow = min(max(a.rpos[qr], (int64_t)0), a.r_rows - 1);
     const bool lo = part < TPR / 2;
     const int i0 = (lo ? part : part - TPR / 2) * DL;
-    const float* cp = reinterpret_cast<const float*>(a.rcos) + crow * a.r_ss + i0;
-    const float* sp = reinterpret_cast<const float*>(a.rsin) + crow * a.r_ss + i0;
+    const T* cp = reinterpret_cast<const T*>(a.rcos) + crow * a.r_ss + i0;
+    const T* sp = reinterpret_cast<const T*>(a.rsin) + crow * a.r_ss + i0;
 #pragma unroll
     for (int i = 0; i < DL; ++i) {
-      const float other = qp[(lo ? part + TPR / 2 : part - TPR / 2) * DL + i];
-      float y1, y2;
-      rope_rotate<float, float>(lo ? qv[i] : other, lo ? other : qv[i], cp[i], sp[i], y1, y2);
-      qv[i] = lo ? y1 : y2;
+      const float other = Elem<T>::to_f32(qp[(lo ? part + TPR / 2 : part - TPR / 2) * DL + i]);
+      T y1, y2;
+      rope_rotate<T, T>(lo ? qv[i] : other, lo ? other : qv[i], cp[i], sp[i], y1, y2);
+      qv[i] = Elem<T>::to_f32(lo ? y1 : y2);
     }
   }
   float m = kNegBig, l = 0.f;
-  const float* kb = reinterpret_cast<const float*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh;
-  const float* vb = reinterpret_cast<const float*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh;
+  const T* kb = reinterpret_cast<const T*>(a.k) + (int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh;
+  const T* vb = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh;
   const int last = min(rb * ROWS + ROWS, a.S) - 1;
   for (int k0 = 0; k0 <= last; k0 += BN) {
     __syncthreads();
-    for (int e = tid; e < BN * D / 4; e += 256) {
-      const int r = e / (D / 4), d = 4 * (e % (D / 4));
+    for (int e = tid; e < BN * D / CN; e += 256) {
+      const int r = e / (D / CN), d = CN * (e % (D / CN));
       const int row = min(k0 + r, a.S - 1);
-      *reinterpret_cast<f4*>(&ks[r][d]) = *reinterpret_cast<const f4*>(kb + (int64_t)row * a.k_ss + d);
-      *reinterpret_cast<f4*>(&vs[r][d]) = *reinterpret_cast<const f4*>(vb + (int64_t)row * a.v_ss + d);
+      float kf[CN], vf[CN];
+      Chunk<T>::unpack(load16(kb + (int64_t)row * a.k_ss + d), kf);
+      Chunk<T>::unpack(load16(vb + (int64_t)row * a.v_ss + d), vf);
+#pragma unroll
+      for (int c = 0; c < CN; c += 4) {
+        *reinterpret_cast<f4*>(&ks[r][d + c]) = f4{kf[c], kf[c + 1], kf[c + 2], kf[c + 3]};
+        *reinterpret_cast<f4*>(&vs[r][d + c]) = f4{vf[c], vf[c + 1], vf[c + 2], vf[c + 3]};
+      }
     }
     __syncthreads();
     const int nk = min(BN, qrow - k0 + 1);  // keys k0..qrow are visible
@@ -1064,11 +1073,11 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillArgs a) {
     }
   }
   if (qrow >= a.S) return;
-  float* op = reinterpret_cast<float*>(a.o) + (int64_t)b * a.o_sb + (int64_t)head * a.o_sh +
-              (int64_t)qrow * a.o_ss + part * DL;
+  T* op = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_sb + (int64_t)head * a.o_sh +
+          (int64_t)qrow * a.o_ss + part * DL;
   const float inv = 1.0f / l;
 #pragma unroll
-  for (int i = 0; i < DL; ++i) op[i] = acc[i] * inv;
+  for (int i = 0; i < DL; ++i) op[i] = Elem<T>::from_f32(acc[i] * inv);
   if (a.lse != nullptr && part == 0)
     a.lse[((int64_t)b * a.Hq + head) * a.S + qrow] = (m + __log2f(l)) * kLn2;
 }
@@ -1082,6 +1091,23 @@ hipError_t launch(const PrefillArgs& a, int nwaves, hipStream_t stream) {
   dim3 block((unsigned)(nwaves * 64));
   const size_t smem = 2 * 2 * 64 * D * sizeof(T);  // 2 buffers x (K + V) tiles
   hipLaunchKernelGGL((prefill_kernel<T, D>), grid, block, smem, stream, a);
+  return hipGetLastError();
+}
+
+// VALU kernel: D/8 lanes per query row, 2048/D rows per 256-thread block.
+template <typename T>
+hipError_t launch_valu(const PrefillArgs& a, int64_t head_dim, hipStream_t st) {
+  const int rows = (int)(2048 / head_dim);
+  const int64_t nblk = (int64_t)a.B * a.Hq * ((a.S + rows - 1) / rows);
+  if (nblk > INT32_MAX) return hipErrorInvalidConfiguration;
+  const dim3 grid((unsigned)nblk), block(256);
+  switch (head_dim) {
+    case 16: hipLaunchKernelGGL((prefill_valu_kernel<T, 16>), grid, block, 0, st, a); break;
+    case 32: hipLaunchKernelGGL((prefill_valu_kernel<T, 32>), grid, block, 0, st, a); break;
+    case 64: hipLaunchKernelGGL((prefill_valu_kernel<T, 64>), grid, block, 0, st, a); break;
+    case 128: hipLaunchKernelGGL((prefill_valu_kernel<T, 128>), grid, block, 0, st, a); break;
+    default: hipLaunchKernelGGL((prefill_valu_kernel<T, 256>), grid, block, 0, st, a); break;
+  }
   return hipGetLastError();
 }
 
@@ -1137,9 +1163,10 @@ int32_t attn_prefill(const void* q, const void* k, const void* v, void* o, float
     set_last_error("attn_prefill: unknown dtype code %d", (int)dtype);
     return MI_ERR_INVALID;
   }
-  if (!(head_dim == 64 || head_dim == 128 || (head_dim == 32 && dtype != MI_DTYPE_F32))) {
-    set_last_error("attn_prefill: head_dim %lld has no kernel (supported: 64, 128; 32 for "
-                   "bf16/fp16)", (long long)head_dim);
+  if (!(head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128 ||
+        head_dim == 256)) {
+    set_last_error("attn_prefill: head_dim %lld has no kernel (supported: 16, 32, 64, 128, "
+                   "256)", (long long)head_dim);
     return MI_ERR_UNSUPPORTED;
   }
   const int64_t eb = dtype == MI_DTYPE_F32 ? 4 : 2;
@@ -1194,14 +1221,10 @@ int32_t attn_prefill(const void* q, const void* k, const void* v, void* o, float
   }
   hipError_t e;
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == MI_DTYPE_F32) {
-    const int rows = 256 / (int)(head_dim / 8);
-    const int64_t nblk = (int64_t)a.B * a.Hq * ((a.S + rows - 1) / rows);
-    if (head_dim == 64)
-      hipLaunchKernelGGL(prefill_f32_kernel<64>, dim3((unsigned)nblk), dim3(256), 0, st, a);
-    else
-      hipLaunchKernelGGL(prefill_f32_kernel<128>, dim3((unsigned)nblk), dim3(256), 0, st, a);
-    e = hipGetLastError();
+  if (dtype == MI_DTYPE_F32 || head_dim == 16 || head_dim == 256) {
+    e = dtype == MI_DTYPE_F32   ? launch_valu<float>(a, head_dim, st)
+        : dtype == MI_DTYPE_BF16 ? launch_valu<bf16_t>(a, head_dim, st)
+                                 : launch_valu<f16_t>(a, head_dim, st);
   } else if (dtype == MI_DTYPE_BF16) {
     e = sp ? launch_sp<bf16_t>(a, st)
            : head_dim == 32 ? launch<bf16_t, 32>(a, nwaves, st) : launch<bf16_t, 128>(a, nwaves, st);

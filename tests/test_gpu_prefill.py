@@ -39,13 +39,15 @@ def test_prefill_matches_oracle(dev, dtype, D, Hq, Hkv, S):
     assert max_abs(lse, ref_lse) < 1e-3
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [16, 32, 256])
 @pytest.mark.parametrize("Hq,Hkv,S", [(8, 2, 77), (16, 16, 256), (4, 1, 130)])
-def test_prefill_head_dim_32(dev, dtype, Hq, Hkv, S):
-    """head_dim 32 (the reference kernel takes any power-of-two head_dim,
-    src/flash_attn.py:29-32), with q's RoPE fused and without."""
+def test_prefill_other_head_dims(dev, dtype, D, Hq, Hkv, S):
+    """head_dim 16, 32 and 256 (the reference kernel takes any power-of-two
+    head_dim, src/flash_attn.py:29-32): bf16/fp16 at 32 on MFMA, the rest on
+    the VALU kernel; with q's RoPE fused and without."""
     from src.rope import apply_rotary
-    B, D = 2, 32
+    B = 2
     q = randn((B, S, Hq, D), 80, dtype, dev).transpose(1, 2)
     k = randn((B, Hkv, S, D), 81, dtype, dev)
     v = randn((B, Hkv, S, D), 82, dtype, dev)
@@ -57,8 +59,9 @@ def test_prefill_head_dim_32(dev, dtype, Hq, Hkv, S):
     assert torch.equal(fused, _fa()(apply_rotary(q, cos, sin), k, v))
 
 
-def test_prefill_head_dim_32_fp32_is_unsupported(dev):
-    q = randn((1, 4, 16, 32), 83, torch.float32, dev)
+@pytest.mark.parametrize("D", [8, 48, 512])
+def test_prefill_head_dim_without_kernel_is_unsupported(dev, D):
+    q = randn((1, 4, 16, D), 83, torch.bfloat16, dev)
     with pytest.raises(NotImplementedError, match="head_dim"):
         _fa()(q, q[:, :1], q[:, :1])
 
