@@ -249,10 +249,12 @@ def bench_config5(torch, steps: int, warmup: int) -> dict:
 
 def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
     """The seven W8A16 projections of one Llama-3.2-1B layer at config 2's token
-    count (M = 4 x 2048), back to back, each through the model's GEMM dispatch
-    (w8a16_gemm_mfma: the split-K form where the tile grid leaves CUs idle)."""
+    count (M = 4 x 2048), back to back, through the model's GEMM dispatch: wq,
+    wk and wv in one mi_w8a16_gemm_multi launch (QuantizedAttention.qkv), the
+    others through w8a16_gemm_mfma (the split-K form where the tile grid
+    leaves CUs idle).  per_projection also times wq, wk and wv one by one."""
     from src import _lib
-    from src.quant_linear import w8a16_gemm_mfma
+    from src.quant_linear import gemm_multi_worth, w8a16_gemm_mfma, w8a16_gemm_multi
     dev = torch.device("cuda:0")
     _lib.load()
     M = 4 * 2048
@@ -267,8 +269,18 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
         _, N, K = shapes[i]
         w8a16_gemm_mfma(xs[K], ws[i], ss[i])
 
+    fuse_qkv = gemm_multi_worth(M, 2048, [N for _, N, _ in shapes[:3]], dev)
+
+    def qkv():
+        if fuse_qkv:
+            w8a16_gemm_multi(xs[2048], [(ws[i], ss[i]) for i in range(3)])
+        else:
+            for i in range(3):
+                call(i)
+
     def step():
-        for i in range(len(shapes)):
+        qkv()
+        for i in range(3, len(shapes)):
             call(i)
 
     def timed(fn, n):
@@ -289,6 +301,9 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
         t = timed(lambda: call(i), steps)
         per[name] = {"N": N, "K": K, "us": round(t * 1e3, 2),
                      "tflops": round(2.0 * M * N * K / (t * 1e-3) / 1e12, 1)}
+    t = timed(qkv, steps)
+    per["wq+wk+wv"] = {"N": 3072, "K": 2048, "us": round(t * 1e3, 2), "one_launch": fuse_qkv,
+                       "tflops": round(2.0 * M * 3072 * 2048 / (t * 1e-3) / 1e12, 1)}
     tf = flops / (ms * 1e-3) / 1e12
     # the dominant shape (w1/w3: 2 of the 7 calls, 54 % of the flops)
     dom = per["w1"]

@@ -321,6 +321,23 @@ int32_t mi_w8a16_gemm_splitk(const void* x, const int8_t* w, const void* scales,
                              void* stream);
 
 /*
+ * n_mats (1..4) GEMMs of the same activation x in one launch, e.g. a layer's
+ * q, k and v projections: y_i = mi_w8a16_gemm(x, w_i, scales_i) for each i,
+ * bit for bit, with the output tiles of all matrices in one grid (no tail
+ * round per matrix).  w, scales and y are host arrays of n_mats device
+ * pointers; n, w_sn, s_sn and y_sm host arrays of n_mats values; each matrix
+ * meets mi_w8a16_gemm's requirements.  Replaces the three
+ * W8A16Linear.forward -> w8a16_gemm_launch calls of a prefill attention block
+ *   src/model.py:54 with src/quant_linear.py:191-247, 250-292.
+ */
+int32_t mi_w8a16_gemm_multi(const void* x, int64_t m, int64_t k, int64_t x_sm,
+                            int32_t n_mats, const int8_t* const* w,
+                            const void* const* scales, void* const* y,
+                            const int64_t* n, const int64_t* w_sn,
+                            const int64_t* s_sn, const int64_t* y_sm,
+                            int32_t dtype, int32_t sdtype, void* stream);
+
+/*
  * Fused decode-step projection (1 <= m <= 16 rows; k one of 512, 1024, 1536,
  * 2048, 3072, 4096, 6144, 8192):
  *   a   = rmsnorm(x, norm_w, eps) if norm_w != NULL else x   (rounded to dtype)

@@ -118,30 +118,27 @@ template <> struct GemmOps<f16_t> {
 // Tile of a linear workgroup id: ids dealt round-robin to the 8 XCDs are first
 // regrouped so that each XCD's ids are consecutive, then consecutive ids walk
 // groups of kGmGroupM m-tiles, m fastest.
-__device__ inline void gm_tile(const GemmArgs& a, int b, int& tm, int& tn) {
-  const int G = a.tiles_m * a.tiles_n;
+__device__ inline void gm_tile(int tiles_m, int tiles_n, int b, int& tm, int& tn) {
+  const int G = tiles_m * tiles_n;
   if ((G & 7) == 0) b = (b & 7) * (G >> 3) + (b >> 3);
-  const int group = kGmGroupM * a.tiles_n;
+  const int group = kGmGroupM * tiles_n;
   const int g = b / group, first = g * kGmGroupM;
-  const int gm = min(a.tiles_m - first, kGmGroupM);
+  const int gm = min(tiles_m - first, kGmGroupM);
   const int in = b - g * group;
   tm = first + in % gm;
   tn = in / gm;
 }
 
+// One workgroup's 128 x 256 output tile (tm, tn) of the GEMM described by a
+// (split-K: the k stages of `split`).
 template <typename T, typename ST, bool PARTIAL>
-__global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
+__device__ __forceinline__ void gemm_tile_body(const GemmArgs& a, int tm, int tn, int split) {
   using OP = GemmOps<T>;
   typedef typename OP::v8 v8;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the wave's 64 columns
   const int r = lane & 31, h = lane >> 5;
-  // split-K: workgroup ids run over all tiles of split 0, then of split 1, ...
-  const int n_tiles = a.tiles_m * a.tiles_n;
-  const int split = PARTIAL ? (int)blockIdx.x / n_tiles : 0;
-  int tm, tn;
-  gm_tile(a, (int)blockIdx.x - split * n_tiles, tm, tn);
   const int m0 = tm * kGmBM, n0 = tn * kGmBN;
 
   // the workgroup's 256 column scales as fp32, staged in LDS after the first
@@ -345,6 +342,40 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
   }
 }
 
+template <typename T, typename ST, bool PARTIAL>
+__global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
+  // split-K: workgroup ids run over all tiles of split 0, then of split 1, ...
+  const int n_tiles = a.tiles_m * a.tiles_n;
+  const int split = PARTIAL ? (int)blockIdx.x / n_tiles : 0;
+  int tm, tn;
+  gm_tile(a.tiles_m, a.tiles_n, (int)blockIdx.x - split * n_tiles, tm, tn);
+  gemm_tile_body<T, ST, PARTIAL>(a, tm, tn, split);
+}
+
+// Several GEMMs of one activation x (e.g. the q, k and v projections) in one
+// launch: the 128 x 256 tiles of all matrices form one grid, matrix i owning
+// tile columns [col0[i], col0[i + 1]); the grid is walked in the single-GEMM
+// order (XCD regrouping, groups of m-tiles), so each XCD's resident tiles
+// share activation rows across the matrices.  Each tile is computed exactly
+// as by w8a16_gemm_kernel on its own matrix.
+constexpr int kGmMaxMats = 4;
+struct GemmMultiArgs {
+  GemmArgs mat[kGmMaxMats];
+  int32_t col0[kGmMaxMats + 1];
+  int32_t n_mats, tiles_m;
+};
+
+template <typename T, typename ST>
+__global__ __launch_bounds__(256, 2) void w8a16_gemm_multi_kernel(GemmMultiArgs ma) {
+  int tm, tn;
+  gm_tile(ma.tiles_m, ma.col0[ma.n_mats], (int)blockIdx.x, tm, tn);
+  int i = 0;
+#pragma unroll
+  for (int j = 1; j < kGmMaxMats; ++j)
+    if (j < ma.n_mats && tn >= ma.col0[j]) i = j;
+  gemm_tile_body<T, ST, false>(ma.mat[i], tm, tn - ma.col0[i], 0);
+}
+
 // Split-K finish: y[m, n] = round((sum over splits, in split order, of
 // part[s][m][n]) * scale[n]); one thread per 4 consecutive columns of a row.
 template <typename T, typename ST>
@@ -436,6 +467,19 @@ void launch_gemm(const GemmArgs& a, int32_t splits, int32_t dtype, int32_t sdtyp
   dim3 grid((unsigned)((int64_t)a.tiles_m * a.tiles_n * splits)), block(256);
 #define MI_GEMM(T, ST) \
   hipLaunchKernelGGL((w8a16_gemm_kernel<T, ST, PARTIAL>), grid, block, kGmLdsBytes, st, a)
+  if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_BF16) MI_GEMM(bf16_t, bf16_t);
+  else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F32) MI_GEMM(bf16_t, float);
+  else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F16) MI_GEMM(bf16_t, f16_t);
+  else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_F16) MI_GEMM(f16_t, f16_t);
+  else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_F32) MI_GEMM(f16_t, float);
+  else MI_GEMM(f16_t, bf16_t);
+#undef MI_GEMM
+}
+
+void launch_multi(const GemmMultiArgs& ma, int32_t dtype, int32_t sdtype, hipStream_t st) {
+  dim3 grid((unsigned)((int64_t)ma.tiles_m * ma.col0[ma.n_mats])), block(256);
+#define MI_GEMM(T, ST) \
+  hipLaunchKernelGGL((w8a16_gemm_multi_kernel<T, ST>), grid, block, kGmLdsBytes, st, ma)
   if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_BF16) MI_GEMM(bf16_t, bf16_t);
   else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F32) MI_GEMM(bf16_t, float);
   else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F16) MI_GEMM(bf16_t, f16_t);
@@ -546,4 +590,42 @@ extern "C" int32_t mi_w8a16_gemm_splitk(const void* x, const int8_t* w, const vo
   if (rc != MI_OK) return rc;
   launch_reduce(a, (int32_t)used, dtype, sdtype, st);
   return launch_status("w8a16_gemm_splitk");
+}
+
+extern "C" int32_t mi_w8a16_gemm_multi(const void* x, int64_t m, int64_t k, int64_t x_sm,
+                                       int32_t n_mats, const int8_t* const* w,
+                                       const void* const* scales, void* const* y,
+                                       const int64_t* n, const int64_t* w_sn,
+                                       const int64_t* s_sn, const int64_t* y_sm,
+                                       int32_t dtype, int32_t sdtype, void* stream) {
+  const char* what = "w8a16_gemm_multi";
+  if (n_mats < 1 || n_mats > kGmMaxMats || w == nullptr || scales == nullptr || y == nullptr ||
+      n == nullptr || w_sn == nullptr || s_sn == nullptr || y_sm == nullptr) {
+    set_last_error("%s: need 1..%d matrices and non-null argument arrays (n_mats=%d)", what,
+                   kGmMaxMats, (int)n_mats);
+    return MI_ERR_INVALID;
+  }
+  if (!dtypes_ok(dtype, sdtype)) {
+    set_last_error("%s: activations must be bf16 or fp16 (dtype %d, scales %d)", what,
+                   (int)dtype, (int)sdtype);
+    return MI_ERR_UNSUPPORTED;
+  }
+  GemmMultiArgs ma{};
+  int64_t cols = 0;
+  for (int i = 0; i < n_mats; ++i) {
+    int32_t rc = gemm_setup(what, x, w[i], scales[i], y[i], m, n[i], k, x_sm, w_sn[i], s_sn[i],
+                            y_sm[i], ma.mat[i]);
+    if (rc != MI_OK) return rc;
+    ma.col0[i] = (int32_t)cols;
+    cols += ma.mat[i].tiles_n;
+  }
+  ma.tiles_m = ma.mat[0].tiles_m;
+  if (ma.tiles_m * cols > INT32_MAX / 64) {
+    set_last_error("%s: too many tiles", what);
+    return MI_ERR_INVALID;
+  }
+  ma.col0[n_mats] = (int32_t)cols;
+  ma.n_mats = n_mats;
+  launch_multi(ma, dtype, sdtype, (hipStream_t)stream);
+  return launch_status(what);
 }

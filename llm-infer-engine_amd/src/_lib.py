@@ -148,6 +148,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _ptr, _i64, _i64,                      # part part_elems splits
         _i32, _i32, _ptr,                      # dtype sdtype stream
     ]),
+    "mi_w8a16_gemm_multi": (_i32, [
+        _ptr, _i64, _i64, _i64, _i32,          # x M K x_sm n_mats
+        _ptr, _ptr, _ptr,                      # w[] scales[] y[] (host arrays)
+        _ptr, _ptr, _ptr, _ptr,                # N[] w_sn[] s_sn[] y_sm[]
+        _i32, _i32, _ptr,                      # dtype sdtype stream
+    ]),
     "mi_w8a16_linear_fused": (_i32, [
         _ptr, _i64, _ptr, _f32,                # x x_sm norm_w eps
         _ptr, _ptr, _i64,                      # w_a s_a w_sn_a

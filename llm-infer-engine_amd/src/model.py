@@ -61,12 +61,16 @@ class Attention(nn.Module):
         self.wv = linear(args.dim, args.n_kv_heads * self.head_dim, bias=False)
         self.wo = linear(args.n_heads * self.head_dim, args.dim, bias=False)
 
+    def qkv(self, x):
+        """The three input projections (src/model.py:54)."""
+        return self.wq(x), self.wk(x), self.wv(x)
+
     def forward(self, x, rope_cos, rope_sin, layer_idx=None, start_pos=0, kv_cache=None,
                 use_cuda_graph=False, scatter_positions=None, decode_attn_mask=None, *,
                 seq_lens=None, rope_by_position=False):
         batch_size, query_len, _ = x.shape
         torch.cuda.nvtx.range_push("QKV_proj")
-        xq, xk, xv = self.wq(x), self.wk(x), self.wv(x)
+        xq, xk, xv = self.qkv(x)
         torch.cuda.nvtx.range_pop()
         xq = xq.view(batch_size, query_len, self.n_heads, self.head_dim).transpose(1, 2)
         xk = xk.view(batch_size, query_len, self.n_kv_heads, self.head_dim).transpose(1, 2)

@@ -16,7 +16,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from . import decode_layer
+from . import decode_layer, quant_linear
 from .flash_decode import flash_decode
 from .model import Attention, FeedForward, Llama3, TransformerBlock
 from .quant_linear import W8A16Linear
@@ -31,6 +31,18 @@ class QuantizedFeedForward(FeedForward):
 class QuantizedAttention(Attention):
     def __init__(self, args):
         super().__init__(args, W8A16Linear)
+
+    def qkv(self, x):
+        """Prefill-sized inputs: wq, wk and wv in one GEMM launch (bitwise the
+        three separate GEMMs without a K split) when their tiles together
+        fill the GPU; otherwise one W8A16Linear call each."""
+        x2 = x.reshape(-1, x.shape[-1])
+        mats = (self.wq, self.wk, self.wv)
+        if not quant_linear.gemm_multi_worth(x2.shape[0], x2.shape[1],
+                                             [m.out_features for m in mats], x.device):
+            return super().qkv(x)
+        ys = quant_linear.w8a16_gemm_multi(x2, [(m.weight, m.scales) for m in mats])
+        return tuple(y.reshape(*x.shape[:-1], m.out_features) for y, m in zip(ys, mats))
 
 
 class QuantizedTransformerBlock(TransformerBlock):

@@ -141,6 +141,57 @@ def w8a16_gemm_mfma(x, weight, scales, *, splits: int | None = None):
     return out
 
 
+_GEMM_TILE_M, _GEMM_TILE_N = 128, 256
+
+
+def gemm_multi_worth(M: int, K: int, out_features, device) -> bool:
+    """Whether one mi_w8a16_gemm_multi launch should serve several projections
+    of the same [M, K] input: the GEMM kernels apply and the 128 x 256 tiles of
+    all matrices together give every CU a workgroup (smaller grids are better
+    served one matrix at a time with K split across workgroups)."""
+    if not gemm_supported(M, K):
+        return False
+    tiles = -(-M // _GEMM_TILE_M) * sum(-(-n // _GEMM_TILE_N) for n in out_features)
+    return tiles >= torch.cuda.get_device_properties(device).multi_processor_count
+
+
+def w8a16_gemm_multi(x, mats):
+    """x [M, K] times each (weight [N_i, K] int8, scales [N_i] or [N_i, 1]) of
+    `mats` (1-4 pairs) in one launch -> [y_i [M, N_i]]; each y_i is bitwise
+    w8a16_gemm_mfma(x, weight_i, scales_i, splits=1)."""
+    import ctypes
+    if not 1 <= len(mats) <= 4:
+        raise ValueError(f"w8a16_gemm_multi takes 1-4 matrices, got {len(mats)}")
+    prepped = [_prep(x, w, s) for w, s in mats]
+    x = prepped[0][0]
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    sdt = {s.dtype for _, _, s in prepped}
+    if len(sdt) != 1:
+        raise TypeError("w8a16_gemm_multi: all scales must share a dtype")
+    M, K = x.shape
+    outs = [torch.empty((M, w.shape[0]), device=x.device, dtype=x.dtype) for _, w, _ in prepped]
+    n = len(prepped)
+    P = ctypes.c_void_p * n
+    I = ctypes.c_int64 * n
+    w_arr = P(*[w.data_ptr() for _, w, _ in prepped])
+    s_arr = P(*[s.data_ptr() for _, _, s in prepped])
+    y_arr = P(*[y.data_ptr() for y in outs])
+    n_arr = I(*[w.shape[0] for _, w, _ in prepped])
+    wsn = I(*[w.stride(0) for _, w, _ in prepped])
+    ssn = I(*[s.stride(0) for _, _, s in prepped])
+    ysm = I(*[y.stride(0) for y in outs])
+    lib = _lib.load()
+    st = lib.mi_w8a16_gemm_multi(
+        x.data_ptr(), M, K, x.stride(0), n,
+        ctypes.addressof(w_arr), ctypes.addressof(s_arr), ctypes.addressof(y_arr),
+        ctypes.addressof(n_arr), ctypes.addressof(wsn), ctypes.addressof(ssn),
+        ctypes.addressof(ysm),
+        _lib.dtype_code(x.dtype), _lib.dtype_code(prepped[0][2].dtype), _lib.stream_of(x))
+    _lib.check(st, "w8a16_gemm_multi")
+    return outs
+
+
 def w8a16_gemm_launch(x, weight, scales, *, block_m: int = 64, block_n: int = 64, block_k: int = 128):
     """Same contract as w8a16_gemv_launch for any M (src/quant_linear.py:191-247).
     block_m/block_n/block_k are accepted for signature compatibility (the

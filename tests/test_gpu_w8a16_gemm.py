@@ -192,3 +192,69 @@ def test_epilogue_store_paths_agree(dev):
     assert torch.equal(ys[0], ys[1][:, :N])
     assert torch.all(ys[1][:, N:] == 3.0)
     assert _rel(ys[0], oq.w8a16(x, q, s)) < 2e-2
+
+
+@pytest.mark.parametrize("M,K,Ns,dtype", [(8192, 2048, (2048, 512, 512), torch.bfloat16),
+                                          (300, 1024, (1000, 256, 77), torch.float16),
+                                          (65, 512, (256,), torch.bfloat16),
+                                          (1030, 640, (512, 1003, 256, 2048), torch.bfloat16)])
+def test_gemm_multi_is_bitwise_the_separate_gemms(dev, M, K, Ns, dtype):
+    """Several matrices of one x in one launch (the q/k/v projections): every
+    output bitwise the unsplit single-matrix GEMM, ragged N included."""
+    from src.quant_linear import w8a16_gemm_mfma, w8a16_gemm_multi
+    mats = [_quantised(N, K, dtype, dev, 20 + i) for i, N in enumerate(Ns)]
+    x = _x(M, K, dtype, dev, 30)
+    ys = w8a16_gemm_multi(x, mats)
+    for (q, s), y, N in zip(mats, ys, Ns):
+        assert y.shape == (M, N) and y.dtype == dtype
+        assert torch.equal(y, w8a16_gemm_mfma(x, q, s, splits=1))
+    q, s = mats[-1]
+    assert _rel(ys[-1], oq.w8a16(x, q, s)) < 2e-2
+
+
+def test_gemm_multi_fp32_scales_and_rejections(dev):
+    from src import _lib
+    from src.quant_linear import w8a16_gemm_mfma, w8a16_gemm_multi
+    M, K = 256, 512
+    mats = [_quantised(N, K, torch.bfloat16, dev, 40 + N) for N in (512, 256)]
+    mats = [(q, s.float()) for q, s in mats]
+    x = _x(M, K, torch.bfloat16, dev, 41)
+    for (q, s), y in zip(mats, w8a16_gemm_multi(x, mats)):
+        assert torch.equal(y, w8a16_gemm_mfma(x, q, s, splits=1))
+    with pytest.raises(ValueError):
+        w8a16_gemm_multi(x, mats * 3)
+    with pytest.raises(TypeError):
+        w8a16_gemm_multi(x, [mats[0], (mats[1][0], mats[1][1].bfloat16())])
+    # K not a multiple of 64: refused before any launch
+    xb = _x(M, 96, torch.bfloat16, dev, 42)
+    qb, sb = _quantised(64, 96, torch.bfloat16, dev, 43)
+    with pytest.raises(Exception, match="multiple of 64"):
+        w8a16_gemm_multi(xb, [(qb, sb)])
+    assert "multiple of 64" in _lib.last_error()
+
+
+def test_quantized_attention_fuses_qkv_at_prefill_sizes(dev):
+    """QuantizedAttention.qkv takes the one-launch path when the tiles fill the
+    GPU (bitwise the unsplit GEMMs) and the per-linear path otherwise."""
+    from src.config import ModelArgs
+    from src.model_quantized import QuantizedAttention
+    from src.quant_linear import gemm_multi_worth, w8a16_gemm_mfma
+    args = ModelArgs(dim=2048, n_layers=1, n_heads=32, n_kv_heads=8, vocab_size=128,
+                     max_batch_size=1, max_seq_len=4096)
+    attn = QuantizedAttention(args).to(dev)
+    for i, lin in enumerate((attn.wq, attn.wk, attn.wv, attn.wo)):
+        q, s = _quantised(lin.out_features, lin.in_features, torch.bfloat16, dev, 50 + i)
+        lin.weight.data.copy_(q)
+        lin.scales.data.copy_(s.view(-1, 1))
+    x = _x(4 * 2048, 2048, torch.bfloat16, dev, 60).view(4, 2048, 2048)
+    assert gemm_multi_worth(4 * 2048, 2048, [2048, 512, 512], dev)
+    xq, xk, xv = attn.qkv(x)
+    for y, lin in zip((xq, xk, xv), (attn.wq, attn.wk, attn.wv)):
+        assert y.shape == (4, 2048, lin.out_features)
+        assert torch.equal(y.view(-1, lin.out_features),
+                           w8a16_gemm_mfma(x.view(-1, 2048), lin.weight, lin.scales, splits=1))
+        assert _rel(y, lin(x)) < 1e-2
+    small = x[:1, :40]
+    assert not gemm_multi_worth(40, 2048, [2048, 512, 512], dev)
+    for y, lin in zip(attn.qkv(small), (attn.wq, attn.wk, attn.wv)):
+        assert torch.equal(y, lin(small))
