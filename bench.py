@@ -250,11 +250,14 @@ def bench_config5(torch, steps: int, warmup: int) -> dict:
 def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
     """The seven W8A16 projections of one Llama-3.2-1B layer at config 2's token
     count (M = 4 x 2048), back to back, through the model's GEMM dispatch: wq,
-    wk and wv in one mi_w8a16_gemm_multi launch (QuantizedAttention.qkv), the
-    others through w8a16_gemm_mfma (the split-K form where the tile grid
-    leaves CUs idle).  per_projection also times wq, wk and wv one by one."""
+    wk and wv in one mi_w8a16_gemm_multi launch (QuantizedAttention.qkv), w1 and
+    w3 with the SwiGLU gating in one mi_w8a16_gemm_swiglu launch
+    (QuantizedFeedForward), wo and w2 through w8a16_gemm_mfma (the split-K form
+    where the tile grid leaves CUs idle).  per_projection also times each
+    projection on its own."""
     from src import _lib
-    from src.quant_linear import gemm_multi_worth, w8a16_gemm_mfma, w8a16_gemm_multi
+    from src.quant_linear import (gemm_multi_worth, swiglu_worth, w8a16_gemm_mfma,
+                                  w8a16_gemm_multi, w8a16_gemm_swiglu)
     dev = torch.device("cuda:0")
     _lib.load()
     M = 4 * 2048
@@ -278,10 +281,23 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
             for i in range(3):
                 call(i)
 
+    fuse_ffn = swiglu_worth(M, 2048, 8192, dev)
+
+    def ffn_chain():   # the op chain of src/model.py:23
+        torch.nn.functional.silu(w8a16_gemm_mfma(xs[2048], ws[4], ss[4])) * \
+            w8a16_gemm_mfma(xs[2048], ws[5], ss[5])
+
+    def ffn_in():
+        if fuse_ffn:
+            w8a16_gemm_swiglu(xs[2048], ws[4], ss[4], ws[5], ss[5])
+        else:
+            ffn_chain()
+
     def step():
         qkv()
-        for i in range(3, len(shapes)):
-            call(i)
+        call(3)
+        ffn_in()
+        call(6)
 
     def timed(fn, n):
         _settle(torch, fn, warmup)
@@ -304,11 +320,17 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
     t = timed(qkv, steps)
     per["wq+wk+wv"] = {"N": 3072, "K": 2048, "us": round(t * 1e3, 2), "one_launch": fuse_qkv,
                        "tflops": round(2.0 * M * 3072 * 2048 / (t * 1e-3) / 1e12, 1)}
+    t = timed(ffn_in, steps)
+    per["silu(w1)*w3"] = {"N": 16384, "K": 2048, "us": round(t * 1e3, 2), "one_launch": fuse_ffn,
+                          "tflops": round(2.0 * M * 16384 * 2048 / (t * 1e-3) / 1e12, 1)}
+    t = timed(ffn_chain, steps)
+    per["silu(w1)*w3 as separate ops"] = {"us": round(t * 1e3, 2)}
     tf = flops / (ms * 1e-3) / 1e12
     # the dominant shape (w1/w3: 2 of the 7 calls, 54 % of the flops)
     dom = per["w1"]
-    out = {"config": "W8A16 prefill projections of one Llama-3.2-1B layer, M = 8192 tokens "
-                     "(config 2's B4 x S2048), bf16 activations, int8 weights, bf16 scales",
+    out = {"config": "W8A16 prefill projections of one Llama-3.2-1B layer as the model runs "
+                     "them (wq|wk|wv one launch, silu(w1)*w3 one launch, wo, w2), M = 8192 "
+                     "tokens (config 2's B4 x S2048), bf16 activations, int8 weights, bf16 scales",
            "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
            "flops_per_step": flops, "per_projection": per,
            "roofline": {"bound": "mfma", "kernel": "w8a16_gemm_kernel (w1 shape)",

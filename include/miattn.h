@@ -321,6 +321,24 @@ int32_t mi_w8a16_gemm_splitk(const void* x, const int8_t* w, const void* scales,
                              void* stream);
 
 /*
+ * The gated feed-forward input of a prefill block in one launch:
+ *   y[m, n] = dtype(dtype(silu(y1)) * y3),  y1 = dtype((x w1^T)[m, n] * s1[n]),
+ *                                           y3 = dtype((x w3^T)[m, n] * s3[n])
+ * (the roundings of w1(x), w3(x), silu and the product as separate ops; silu
+ * is evaluated with the hardware exp2 and reciprocal, so an element can be
+ * one unit in the last place off the separate ops' result), with w1 and w3
+ * [n, k] int8 and everything else as mi_w8a16_gemm; neither projection is
+ * written out.  Replaces silu(self.w1(x)) * self.w3(x) of the
+ * W8A16 feed-forward  src/model.py:23, src/quant_linear.py:191-292.
+ */
+int32_t mi_w8a16_gemm_swiglu(const void* x, const int8_t* w1, const void* scales1,
+                             const int8_t* w3, const void* scales3, void* y,
+                             int64_t m, int64_t n, int64_t k, int64_t x_sm,
+                             int64_t w1_sn, int64_t s1_sn, int64_t w3_sn,
+                             int64_t s3_sn, int64_t y_sm, int32_t dtype,
+                             int32_t sdtype, void* stream);
+
+/*
  * n_mats (1..4) GEMMs of the same activation x in one launch, e.g. a layer's
  * q, k and v projections: y_i = mi_w8a16_gemm(x, w_i, scales_i) for each i,
  * bit for bit, with the output tiles of all matrices in one grid (no tail

@@ -121,6 +121,8 @@ __device__ inline float shfl_xor_f32(float x, int mask) {
 
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ inline float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+// silu in fp32 (x * sigmoid(x) as x / (1 + e^-x)), the form torch's silu uses
+__device__ inline float silu_f32(float a) { return a / (1.0f + expf(-a)); }
 
 __device__ inline u32x4 load16(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);

@@ -96,7 +96,6 @@ __device__ inline V8 i8x8_cvt(uint32_t lo, uint32_t hi) {
   return r;
 }
 
-__device__ inline float silu_f32(float a) { return a / (1.0f + expf(-a)); }
 
 // x from lane (lane ^ OFF) without LDS traffic: a DPP row rotate for 8 (a
 // 16-lane row rotated by 8 is the xor), the gfx950 permlane swaps for 16 and 32.

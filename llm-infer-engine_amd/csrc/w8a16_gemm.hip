@@ -55,6 +55,11 @@ struct GemmArgs {
   int32_t split_stages;
   int32_t part_vec;        // part rows allow 16-byte stores of 4 columns
   int32_t y_line;          // y and its rows are 16-byte aligned (whole-line epilogue)
+  // SwiGLU form: y = silu(x w^T * s) * (x w3^T * s3), each product rounded to
+  // the activation dtype first (w3 / scales3 / strides as w / scales)
+  const unsigned char* w3;
+  const void* scales3;
+  int64_t w3_sn, s3_sn;
 };
 
 constexpr int kGmBM = 128;                      // output rows (m) per workgroup
@@ -65,6 +70,12 @@ constexpr int kGmXDma = kGmXBytes / 1024 / 4;   // 1 KB DMA instructions per wav
 constexpr int kGmGroupM = 8;                    // m-tiles per tile group
 // LDS: two activation stages, then the workgroup's column scales (fp32)
 constexpr size_t kGmLdsBytes = 2 * kGmXBytes + kGmBN * sizeof(float);
+
+// silu(x) = x / (1 + e^-x) with the hardware exp2 and reciprocal (a few ulp
+// of fp32; the SwiGLU epilogue rounds it to the activation dtype right after)
+__device__ inline float silu_fast(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.44269504f));
+}
 
 // chunk swizzle of activation row r (8 chunks of 16 bytes per row)
 __device__ inline int gm_xswz(int r) { return ((r >> 1) ^ (r << 2)) & 7; }
@@ -130,22 +141,32 @@ __device__ inline void gm_tile(int tiles_m, int tiles_n, int b, int& tm, int& tn
 }
 
 // One workgroup's 128 x 256 output tile (tm, tn) of the GEMM described by a
-// (split-K: the k stages of `split`).
-template <typename T, typename ST, bool PARTIAL>
+// (split-K: the k stages of `split`).  SWIGLU: the tile is 128 columns of the
+// gated product, its 256 weight rows the 128 matching rows of w and of w3
+// (each wave: 32 rows of each), combined in the epilogue.
+template <typename T, typename ST, bool PARTIAL, bool SWIGLU = false>
 __device__ __forceinline__ void gemm_tile_body(const GemmArgs& a, int tm, int tn, int split) {
+  static_assert(!(PARTIAL && SWIGLU), "the SwiGLU epilogue needs the whole K");
   using OP = GemmOps<T>;
   typedef typename OP::v8 v8;
   extern __shared__ __align__(16) unsigned char smem_raw[];
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // the wave's 64 columns
   const int r = lane & 31, h = lane >> 5;
-  const int m0 = tm * kGmBM, n0 = tn * kGmBN;
+  const int m0 = tm * kGmBM, n0 = tn * (SWIGLU ? kGmBN / 2 : kGmBN);
 
   // the workgroup's 256 column scales as fp32, staged in LDS after the first
   // stage's copies are issued (read by the epilogue; published by the main
   // loop's first barrier)
-  const ST sc_raw =
-      reinterpret_cast<const ST*>(a.scales)[(int64_t)min(n0 + (int)threadIdx.x, a.N - 1) * a.s_sn];
+  ST sc_raw;
+  if constexpr (SWIGLU) {   // [0, 128): w's scales, [128, 256): w3's
+    const bool hi = threadIdx.x >= kGmBN / 2;
+    const int c = min(n0 + (int)(threadIdx.x & (kGmBN / 2 - 1)), a.N - 1);
+    sc_raw = hi ? reinterpret_cast<const ST*>(a.scales3)[(int64_t)c * a.s3_sn]
+                : reinterpret_cast<const ST*>(a.scales)[(int64_t)c * a.s_sn];
+  } else {
+    sc_raw = reinterpret_cast<const ST*>(a.scales)[(int64_t)min(n0 + (int)threadIdx.x, a.N - 1) * a.s_sn];
+  }
   float* const sc_lds = reinterpret_cast<float*>(smem_raw + 2 * kGmXBytes);
 
   // ---- activation DMA: instruction i of wave wv copies tile rows
@@ -175,8 +196,12 @@ __device__ __forceinline__ void gemm_tile_body(const GemmArgs& a, int tm, int tn
   // past N clamped, never stored).
   const unsigned char* w_row[2];
 #pragma unroll
-  for (int nf = 0; nf < 2; ++nf)
-    w_row[nf] = a.w + (int64_t)min(n0 + 64 * wv + 32 * nf + r, a.N - 1) * a.w_sn + 32 * h;
+  for (int nf = 0; nf < 2; ++nf) {
+    if constexpr (SWIGLU)   // fragment 0 from w, 1 from w3: the same 32 output columns
+      w_row[nf] = (nf ? a.w3 : a.w) + (int64_t)min(n0 + 32 * wv + r, a.N - 1) * (nf ? a.w3_sn : a.w_sn) + 32 * h;
+    else
+      w_row[nf] = a.w + (int64_t)min(n0 + 64 * wv + 32 * nf + r, a.N - 1) * a.w_sn + 32 * h;
+  }
   auto load_w = [&](int s, u32x4 (&q)[2][2]) {
 #pragma unroll
     for (int nf = 0; nf < 2; ++nf)
@@ -277,6 +302,74 @@ __device__ __forceinline__ void gemm_tile_body(const GemmArgs& a, int tm, int tn
     return;
   }
   T* y = reinterpret_cast<T*>(a.y);
+  if constexpr (SWIGLU) {
+    // acc[mf][0] / acc[mf][1]: w / w3 products of the same 4 columns per g,
+    // rounded where the unfused chain rounds: y1, y3, silu(y1), the product
+    // (silu with the hardware exp2 and reciprocal: within an ulp of the
+    // chain's bits)
+    auto rnd = [](float v) { return Elem<T>::to_f32(Elem<T>::from_f32(v)); };
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    auto gate4 = [&](int mf, int g, const f32x4& s1, const f32x4& s3) {
+      t4 v;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float y1 = rnd(acc[mf][0][4 * g + i] * s1[i]);
+        const float y3 = rnd(acc[mf][1][4 * g + i] * s3[i]);
+        v[i] = Elem<T>::from_f32(rnd(silu_fast(y1)) * y3);
+      }
+      return v;
+    };
+    if (a.y_line && n0 + kGmBN / 2 <= a.N) {
+      // whole-line stores as below: each wave stages its 32 columns of 32
+      // rows at a time and writes a row's 64 bytes with 4 lanes x 16 bytes
+      constexpr int RS = 80;                 // staged row stride (bytes, padded)
+      block_sync_lds();
+      unsigned char* const stg = smem_raw + wv * 32 * RS;
+      f32x4 s1[4], s3[4];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        s1[g] = *reinterpret_cast<const f32x4*>(sc_lds + 32 * wv + 8 * g + 4 * h);
+        s3[g] = *reinterpret_cast<const f32x4*>(sc_lds + kGmBN / 2 + 32 * wv + 8 * g + 4 * h);
+      }
+#pragma unroll
+      for (int mf = 0; mf < 4; ++mf) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<t4*>(stg + r * RS + (8 * g + 4 * h) * 2) = gate4(mf, g, s1[g], s3[g]);
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's own rows are staged
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int rr = 16 * i + (lane >> 2), cc = lane & 3;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * RS + cc * 16);
+          const int m = m0 + 32 * mf + rr;
+          if (m < a.M)
+            *reinterpret_cast<u32x4*>(y + (int64_t)m * a.y_sm + n0 + 32 * wv + 8 * cc) = v;
+        }
+      }
+      return;
+    }
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int nl = 32 * wv + 8 * g + 4 * h, nb = n0 + nl;
+      const f32x4 s1 = *reinterpret_cast<const f32x4*>(sc_lds + nl);
+      const f32x4 s3 = *reinterpret_cast<const f32x4*>(sc_lds + kGmBN / 2 + nl);
+#pragma unroll
+      for (int mf = 0; mf < 4; ++mf) {
+        const int m = m0 + 32 * mf + r;
+        if (m >= a.M) continue;
+        const t4 v = gate4(mf, g, s1, s3);
+        T* yp = y + (int64_t)m * a.y_sm + nb;
+        if (a.y_vec && nb + 3 < a.N) {
+          *reinterpret_cast<t4*>(yp) = v;
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (nb + i < a.N) yp[i] = v[i];
+        }
+      }
+    }
+    return;
+  }
   if (a.y_line && n0 + kGmBN <= a.N) {
     // Whole-line stores: each wave stages its 64 columns of 32 rows at a time
     // in LDS (the activation stages, free once every wave has read the last
@@ -350,6 +443,16 @@ __global__ __launch_bounds__(256, 2) void w8a16_gemm_kernel(GemmArgs a) {
   int tm, tn;
   gm_tile(a.tiles_m, a.tiles_n, (int)blockIdx.x - split * n_tiles, tm, tn);
   gemm_tile_body<T, ST, PARTIAL>(a, tm, tn, split);
+}
+
+// The gated feed-forward input projection silu(x w1^T) * (x w3^T) in one
+// GEMM: 128-column tiles of the product, each reading the matching rows of w1
+// and w3, so neither projection is written out.
+template <typename T, typename ST>
+__global__ __launch_bounds__(256, 2) void w8a16_gemm_swiglu_kernel(GemmArgs a) {
+  int tm, tn;
+  gm_tile(a.tiles_m, a.tiles_n, (int)blockIdx.x, tm, tn);
+  gemm_tile_body<T, ST, false, true>(a, tm, tn, 0);
 }
 
 // Several GEMMs of one activation x (e.g. the q, k and v projections) in one
@@ -480,6 +583,19 @@ void launch_multi(const GemmMultiArgs& ma, int32_t dtype, int32_t sdtype, hipStr
   dim3 grid((unsigned)((int64_t)ma.tiles_m * ma.col0[ma.n_mats])), block(256);
 #define MI_GEMM(T, ST) \
   hipLaunchKernelGGL((w8a16_gemm_multi_kernel<T, ST>), grid, block, kGmLdsBytes, st, ma)
+  if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_BF16) MI_GEMM(bf16_t, bf16_t);
+  else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F32) MI_GEMM(bf16_t, float);
+  else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F16) MI_GEMM(bf16_t, f16_t);
+  else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_F16) MI_GEMM(f16_t, f16_t);
+  else if (dtype == MI_DTYPE_F16 && sdtype == MI_DTYPE_F32) MI_GEMM(f16_t, float);
+  else MI_GEMM(f16_t, bf16_t);
+#undef MI_GEMM
+}
+
+void launch_swiglu(const GemmArgs& a, int32_t dtype, int32_t sdtype, hipStream_t st) {
+  dim3 grid((unsigned)((int64_t)a.tiles_m * a.tiles_n)), block(256);
+#define MI_GEMM(T, ST) \
+  hipLaunchKernelGGL((w8a16_gemm_swiglu_kernel<T, ST>), grid, block, kGmLdsBytes, st, a)
   if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_BF16) MI_GEMM(bf16_t, bf16_t);
   else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F32) MI_GEMM(bf16_t, float);
   else if (dtype == MI_DTYPE_BF16 && sdtype == MI_DTYPE_F16) MI_GEMM(bf16_t, f16_t);
@@ -627,5 +743,42 @@ extern "C" int32_t mi_w8a16_gemm_multi(const void* x, int64_t m, int64_t k, int6
   ma.col0[n_mats] = (int32_t)cols;
   ma.n_mats = n_mats;
   launch_multi(ma, dtype, sdtype, (hipStream_t)stream);
+  return launch_status(what);
+}
+
+extern "C" int32_t mi_w8a16_gemm_swiglu(const void* x, const int8_t* w1, const void* scales1,
+                                        const int8_t* w3, const void* scales3, void* y,
+                                        int64_t m, int64_t n, int64_t k, int64_t x_sm,
+                                        int64_t w1_sn, int64_t s1_sn, int64_t w3_sn,
+                                        int64_t s3_sn, int64_t y_sm, int32_t dtype,
+                                        int32_t sdtype, void* stream) {
+  const char* what = "w8a16_gemm_swiglu";
+  GemmArgs a;
+  int32_t rc = gemm_setup(what, x, w1, scales1, y, m, n, k, x_sm, w1_sn, s1_sn, y_sm, a);
+  if (rc != MI_OK) return rc;
+  if (w3 == nullptr || scales3 == nullptr) {
+    set_last_error("%s: null pointer", what);
+    return MI_ERR_INVALID;
+  }
+  if (w3_sn < k || w3_sn > (1LL << 23) || (uintptr_t)w3 % 16 != 0 || w3_sn % 16 != 0) {
+    set_last_error("%s: w3 rows must cover K, be 16-byte aligned and below 2^23 bytes apart",
+                   what);
+    return MI_ERR_INVALID;
+  }
+  if (!dtypes_ok(dtype, sdtype)) {
+    set_last_error("%s: activations must be bf16 or fp16 (dtype %d, scales %d)", what,
+                   (int)dtype, (int)sdtype);
+    return MI_ERR_UNSUPPORTED;
+  }
+  a.tiles_n = (int32_t)((n + kGmBN / 2 - 1) / (kGmBN / 2));
+  if ((int64_t)a.tiles_m * a.tiles_n > INT32_MAX / 64) {
+    set_last_error("%s: too many tiles", what);
+    return MI_ERR_INVALID;
+  }
+  a.w3 = reinterpret_cast<const unsigned char*>(w3);
+  a.scales3 = scales3;
+  a.w3_sn = w3_sn;
+  a.s3_sn = s3_sn;
+  launch_swiglu(a, dtype, sdtype, (hipStream_t)stream);
   return launch_status(what);
 }

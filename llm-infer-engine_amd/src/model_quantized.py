@@ -27,6 +27,20 @@ class QuantizedFeedForward(FeedForward):
     def __init__(self, dim: int, hidden_dim: int):
         super().__init__(dim, hidden_dim, W8A16Linear)
 
+    def forward(self, x):
+        """Prefill-sized inputs: silu(w1(x)) * w3(x) in one GEMM launch (the
+        same rounding points, neither projection written out) when its tiles
+        fill the GPU; otherwise the op chain of src/model.py:23."""
+        x2 = x.reshape(-1, x.shape[-1])
+        w1, w3 = self.w1, self.w3
+        if not quant_linear.swiglu_worth(x2.shape[0], x2.shape[1], w1.out_features, x.device):
+            return super().forward(x)
+        torch.cuda.nvtx.range_push("FFN")
+        h = quant_linear.w8a16_gemm_swiglu(x2, w1.weight, w1.scales, w3.weight, w3.scales)
+        out = self.w2(h.view(*x.shape[:-1], w1.out_features))
+        torch.cuda.nvtx.range_pop()
+        return out
+
 
 class QuantizedAttention(Attention):
     def __init__(self, args):

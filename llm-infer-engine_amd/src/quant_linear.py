@@ -192,6 +192,39 @@ def w8a16_gemm_multi(x, mats):
     return outs
 
 
+def swiglu_worth(M: int, K: int, N: int, device) -> bool:
+    """Whether w8a16_gemm_swiglu should serve a W8A16 feed-forward input of
+    [M, K] rows: the GEMM kernels apply and its 128 x 128 tiles of the gated
+    product give every CU a workgroup."""
+    if not gemm_supported(M, K):
+        return False
+    tiles = -(-M // _GEMM_TILE_M) * -(-N // (_GEMM_TILE_N // 2))
+    return tiles >= torch.cuda.get_device_properties(device).multi_processor_count
+
+
+def w8a16_gemm_swiglu(x, w1, s1, w3, s3):
+    """silu(x w1^T * s1) * (x w3^T * s3) in one launch, x [M, K] -> [M, N],
+    rounded where silu(w8a16(x, w1, s1)) * w8a16(x, w3, s3) rounds (silu from
+    the hardware exp2 and reciprocal: an element may be one ulp off)."""
+    x, w1, s1 = _prep(x, w1, s1)
+    _, w3, s3 = _prep(x, w3, s3)
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    if w3.shape != w1.shape:
+        raise ValueError(f"w1 and w3 shapes differ: {tuple(w1.shape)} and {tuple(w3.shape)}")
+    if s1.dtype != s3.dtype:
+        raise TypeError("w8a16_gemm_swiglu: s1 and s3 must share a dtype")
+    M, K = x.shape
+    N = w1.shape[0]
+    out = torch.empty((M, N), device=x.device, dtype=x.dtype)
+    st = _lib.load().mi_w8a16_gemm_swiglu(
+        x.data_ptr(), w1.data_ptr(), s1.data_ptr(), w3.data_ptr(), s3.data_ptr(), out.data_ptr(),
+        M, N, K, x.stride(0), w1.stride(0), s1.stride(0), w3.stride(0), s3.stride(0),
+        out.stride(0), _lib.dtype_code(x.dtype), _lib.dtype_code(s1.dtype), _lib.stream_of(x))
+    _lib.check(st, "w8a16_gemm_swiglu")
+    return out
+
+
 def w8a16_gemm_launch(x, weight, scales, *, block_m: int = 64, block_n: int = 64, block_k: int = 128):
     """Same contract as w8a16_gemv_launch for any M (src/quant_linear.py:191-247).
     block_m/block_n/block_k are accepted for signature compatibility (the

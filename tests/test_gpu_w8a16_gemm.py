@@ -258,3 +258,49 @@ def test_quantized_attention_fuses_qkv_at_prefill_sizes(dev):
     assert not gemm_multi_worth(40, 2048, [2048, 512, 512], dev)
     for y, lin in zip(attn.qkv(small), (attn.wq, attn.wk, attn.wv)):
         assert torch.equal(y, lin(small))
+
+
+@pytest.mark.parametrize("M,K,N,dtype,sdtype", [(8192, 2048, 8192, torch.bfloat16, torch.bfloat16),
+                                                (300, 1024, 1000, torch.float16, torch.float16),
+                                                (65, 512, 200, torch.bfloat16, torch.float32)])
+def test_gemm_swiglu_is_the_unfused_chain(dev, M, K, N, dtype, sdtype):
+    """silu(w1(x)) * w3(x) in one launch: the GEMM outputs are the unsplit
+    single GEMM's bits, then silu and the product are rounded where separate
+    ops round; against that chain on the CPU (the kernel's silu uses the
+    hardware exp2 and reciprocal, so a few elements may be an ulp off) and the
+    fp32 oracle."""
+    from src.quant_linear import w8a16_gemm_mfma, w8a16_gemm_swiglu
+    q1, s1 = _quantised(N, K, dtype, dev, 70)
+    q3, s3 = _quantised(N, K, dtype, dev, 71)
+    s1, s3 = s1.to(sdtype), s3.to(sdtype)
+    x = _x(M, K, dtype, dev, 72)
+    y = w8a16_gemm_swiglu(x, q1, s1, q3, s3)
+    assert y.shape == (M, N) and y.dtype == dtype
+    y1 = w8a16_gemm_mfma(x, q1, s1, splits=1).cpu().float()
+    y3 = w8a16_gemm_mfma(x, q3, s3, splits=1).cpu().float()
+    chain = (torch.nn.functional.silu(y1).to(dtype).float() * y3).to(dtype)
+    yc = y.cpu()
+    assert (yc == chain).float().mean() > 0.99
+    assert _rel(yc, chain) < 1e-2
+    ref = torch.nn.functional.silu(oq.w8a16(x, q1, s1).float()) * oq.w8a16(x, q3, s3).float()
+    assert _rel(yc, ref) < 3e-2
+
+
+def test_quantized_feed_forward_fuses_at_prefill_sizes(dev):
+    from src.model import FeedForward
+    from src.model_quantized import QuantizedFeedForward
+    from src.quant_linear import swiglu_worth
+    ff = QuantizedFeedForward(2048, 8192).to(dev)
+    for i, lin in enumerate((ff.w1, ff.w2, ff.w3)):
+        q, s = _quantised(lin.out_features, lin.in_features, torch.bfloat16, dev, 80 + i)
+        lin.weight.data.copy_(q)
+        lin.scales.data.copy_(s.view(-1, 1))
+    x = _x(2 * 1024, 2048, torch.bfloat16, dev, 90).view(2, 1024, 2048)
+    assert swiglu_worth(2048, 2048, 8192, dev)
+    fused = ff(x)
+    chain = FeedForward.forward(ff, x)
+    assert fused.shape == chain.shape == (2, 1024, 2048)
+    assert _rel(fused, chain) < 1e-2
+    small = x[:1, :40]
+    assert not swiglu_worth(40, 2048, 8192, dev)
+    assert torch.equal(ff(small), FeedForward.forward(ff, small))
