@@ -68,6 +68,40 @@ def test_prefill_then_decode_matches_oracle(dev, quantized):
 
 
 @torch.no_grad()
+def test_w8a16_prefill_with_one_launch_projections(dev, monkeypatch):
+    """At prefill sizes (here 2 x 2048 tokens at Llama-3.2-1B widths) the W8A16
+    block runs q|k|v as one GEMM launch and silu(w1)*w3 as one launch: the
+    prefill's logits and KV cache match the per-projection op chain within
+    the output bar, and the decode step that follows matches the oracle."""
+    from src import quant_linear
+    from src.kv_cache import KVCache
+    args = _small_args(dev, dim=2048, n_layers=1, n_heads=32, n_kv_heads=8, hidden_dim=8192,
+                       vocab_size=1000, max_batch_size=2, max_seq_len=2112)
+    model = _small_model(args, quantized=True)
+    B, S = 2, 2048
+    assert quant_linear.gemm_multi_worth(B * S, args.dim, [2048, 512, 512], dev)
+    assert quant_linear.swiglu_worth(B * S, args.dim, args.hidden_dim, dev)
+    tokens = torch.randint(0, args.vocab_size, (B, S), generator=torch.Generator().manual_seed(3)).to(dev)
+    runs = []
+    for fused in (True, False):
+        if not fused:
+            monkeypatch.setattr(quant_linear, "gemm_multi_worth", lambda *a: False)
+            monkeypatch.setattr(quant_linear, "swiglu_worth", lambda *a: False)
+        kv = KVCache(args, dtype=torch.bfloat16)
+        logits = model(tokens, start_pos=0, kv_cache=kv)
+        runs.append((logits, kv))
+    (lf, kvf), (lc, kvc) = runs
+    _logit_check(lf[:, -1], lc[:, -1])
+    for a, b in ((kvf.k[:, :B, :, :S], kvc.k[:, :B, :, :S]), (kvf.v[:, :B, :, :S], kvc.v[:, :B, :, :S])):
+        assert max_abs(a, b) < 2e-2 * float(b.abs().max())
+    monkeypatch.undo()
+    tok = torch.randint(0, args.vocab_size, (B, 1), generator=torch.Generator().manual_seed(4))
+    ck, cv = kvf.k.cpu(), kvf.v.cpu()
+    logits = model(tok.to(dev), start_pos=S, kv_cache=kvf)
+    _logit_check(logits, omodel.decode_step(model, tok, S, ck, cv, args.norm_eps))
+
+
+@torch.no_grad()
 def test_graph_runner_matches_eager(dev):
     from src.cuda_graph import CUDAGraphDecodeRunner
     from src.kv_cache import KVCache
