@@ -321,6 +321,22 @@ int32_t mi_w8a16_gemm_splitk(const void* x, const int8_t* w, const void* scales,
                              void* stream);
 
 /*
+ * mi_w8a16_gemm (splits <= 1) or mi_w8a16_gemm_splitk (splits >= 2, with its
+ * workspace) with the block's residual added in the epilogue:
+ *   y[m, n] = dtype(res[m, n] + dtype((sum_k x[m,k] w[n,k]) * scales[n]))
+ * (the roundings of the projection and of the add as separate ops); res
+ * [m, n] in x's dtype, unit column stride, row stride res_sm (>= n).
+ * Replaces h = x + self.wo(attn) and out = h + self.w2(...) of a prefill
+ * block  src/model.py:113-127 with src/quant_linear.py:191-292.
+ */
+int32_t mi_w8a16_gemm_residual(const void* x, const int8_t* w, const void* scales,
+                               const void* res, void* y, int64_t m, int64_t n,
+                               int64_t k, int64_t x_sm, int64_t w_sn, int64_t s_sn,
+                               int64_t res_sm, int64_t y_sm, float* part,
+                               int64_t part_elems, int64_t splits, int32_t dtype,
+                               int32_t sdtype, void* stream);
+
+/*
  * The gated feed-forward input of a prefill block in one launch:
  *   y[m, n] = dtype(dtype(silu(y1)) * y3),  y1 = dtype((x w1^T)[m, n] * s1[n]),
  *                                           y3 = dtype((x w3^T)[m, n] * s3[n])

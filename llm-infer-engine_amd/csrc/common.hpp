@@ -42,7 +42,14 @@ template <> struct Elem<bf16_t> {
 template <> struct Elem<f16_t> {
   static constexpr int kBytes = 2;
   __device__ static inline float to_f32(f16_t x) { return (float)x; }
-  __device__ static inline f16_t from_f32(float x) { return (f16_t)x; }
+  // x is materialised as fp32 first: the conversion of a product or sum is
+  // otherwise selected as one v_fma_mixlo_f16 (a single rounding of the exact
+  // result) where the fp32 operation and the conversion round twice, as the
+  // separate ops do
+  __device__ static inline f16_t from_f32(float x) {
+    __asm__("" : "+v"(x));
+    return (f16_t)x;
+  }
 };
 template <> struct Elem<float> {
   static constexpr int kBytes = 4;

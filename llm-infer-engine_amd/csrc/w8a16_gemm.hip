@@ -60,7 +60,25 @@ struct GemmArgs {
   const unsigned char* w3;
   const void* scales3;
   int64_t w3_sn, s3_sn;
+  // residual form (res != nullptr): y = round(res + round(x w^T * s)), res [M, N]
+  // in the activation dtype with unit column stride, rows res_sm elements apart
+  const void* res;
+  int64_t res_sm;
+  int32_t res_line;        // res and its rows are 16-byte aligned
 };
+
+// 8 activation-dtype values a and b (16 bytes each): round(a + b) per element
+template <typename T>
+__device__ inline u32x4 add8(const u32x4& a, const u32x4& b) {
+  float fa[8], fb[8];
+  Chunk<T>::unpack(a, fa);
+  Chunk<T>::unpack(b, fb);
+  typedef T t8 __attribute__((ext_vector_type(8)));
+  t8 o;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = Elem<T>::from_f32(fa[e] + fb[e]);
+  return __builtin_bit_cast(u32x4, o);
+}
 
 constexpr int kGmBM = 128;                      // output rows (m) per workgroup
 constexpr int kGmBN = 256;                      // output columns (n) per workgroup
@@ -370,7 +388,7 @@ __device__ __forceinline__ void gemm_tile_body(const GemmArgs& a, int tm, int tn
     }
     return;
   }
-  if (a.y_line && n0 + kGmBN <= a.N) {
+  if (a.y_line && (a.res == nullptr || a.res_line) && n0 + kGmBN <= a.N) {
     // Whole-line stores: each wave stages its 64 columns of 32 rows at a time
     // in LDS (the activation stages, free once every wave has read the last
     // one) and writes each row's 128 bytes with 8 lanes x 16 bytes of one
@@ -400,10 +418,14 @@ __device__ __forceinline__ void gemm_tile_body(const GemmArgs& a, int tm, int tn
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int rr = 8 * i + (lane >> 3), cc = lane & 7;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * RS + cc * 16);
+        u32x4 v = *reinterpret_cast<const u32x4*>(stg + rr * RS + cc * 16);
         const int m = m0 + 32 * mf + rr;
-        if (m < a.M)
-          *reinterpret_cast<u32x4*>(y + (int64_t)m * a.y_sm + n0 + 64 * wv + 8 * cc) = v;
+        if (m < a.M) {
+          const int64_t col = n0 + 64 * wv + 8 * cc;
+          if (a.res != nullptr)
+            v = add8<T>(v, load16(reinterpret_cast<const T*>(a.res) + (int64_t)m * a.res_sm + col));
+          *reinterpret_cast<u32x4*>(y + (int64_t)m * a.y_sm + col) = v;
+        }
       }
     }
     return;
@@ -419,16 +441,23 @@ __device__ __forceinline__ void gemm_tile_body(const GemmArgs& a, int tm, int tn
         const int m = m0 + 32 * mf + r;
         if (m >= a.M) continue;
         T* yp = y + (int64_t)m * a.y_sm + nb;
+        const T* rp = a.res != nullptr
+                          ? reinterpret_cast<const T*>(a.res) + (int64_t)m * a.res_sm + nb
+                          : nullptr;
+        auto outv = [&](int i) {
+          const T v = Elem<T>::from_f32(acc[mf][nf][4 * g + i] * s4[i]);
+          return a.res != nullptr ? Elem<T>::from_f32(Elem<T>::to_f32(rp[i]) + Elem<T>::to_f32(v)) : v;
+        };
         if (a.y_vec && nb + 3 < a.N) {
           typedef T t4 __attribute__((ext_vector_type(4)));
           t4 v;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] = Elem<T>::from_f32(acc[mf][nf][4 * g + i] * s4[i]);
+          for (int i = 0; i < 4; ++i) v[i] = outv(i);
           *reinterpret_cast<t4*>(yp) = v;
         } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            if (nb + i < a.N) yp[i] = Elem<T>::from_f32(acc[mf][nf][4 * g + i] * s4[i]);
+            if (nb + i < a.N) yp[i] = outv(i);
         }
       }
     }
@@ -497,8 +526,13 @@ __global__ __launch_bounds__(256) void w8a16_splitk_reduce_kernel(GemmArgs a, in
     typedef T t4 __attribute__((ext_vector_type(4)));
     t4 v;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 4; ++i) {
       v[i] = Elem<T>::from_f32(t[i] * Elem<ST>::to_f32(sc[(int64_t)(nb + i) * a.s_sn]));
+      if (a.res != nullptr)
+        v[i] = Elem<T>::from_f32(
+            Elem<T>::to_f32(reinterpret_cast<const T*>(a.res)[(int64_t)m * a.res_sm + nb + i]) +
+            Elem<T>::to_f32(v[i]));
+    }
     if (a.y_vec) {
       *reinterpret_cast<t4*>(yp) = v;
     } else {
@@ -509,7 +543,12 @@ __global__ __launch_bounds__(256) void w8a16_splitk_reduce_kernel(GemmArgs a, in
     for (int i = 0; i < 4 && nb + i < a.N; ++i) {
       float t = pp[i];
       for (int sp = 1; sp < splits; ++sp) t += pp[i + sp * plane];
-      yp[i] = Elem<T>::from_f32(t * Elem<ST>::to_f32(sc[(int64_t)(nb + i) * a.s_sn]));
+      T v = Elem<T>::from_f32(t * Elem<ST>::to_f32(sc[(int64_t)(nb + i) * a.s_sn]));
+      if (a.res != nullptr)
+        v = Elem<T>::from_f32(
+            Elem<T>::to_f32(reinterpret_cast<const T*>(a.res)[(int64_t)m * a.res_sm + nb + i]) +
+            Elem<T>::to_f32(v));
+      yp[i] = v;
     }
   }
 }
@@ -780,5 +819,55 @@ extern "C" int32_t mi_w8a16_gemm_swiglu(const void* x, const int8_t* w1, const v
   a.w3_sn = w3_sn;
   a.s3_sn = s3_sn;
   launch_swiglu(a, dtype, sdtype, (hipStream_t)stream);
+  return launch_status(what);
+}
+
+extern "C" int32_t mi_w8a16_gemm_residual(const void* x, const int8_t* w, const void* scales,
+                                          const void* res, void* y, int64_t m, int64_t n,
+                                          int64_t k, int64_t x_sm, int64_t w_sn, int64_t s_sn,
+                                          int64_t res_sm, int64_t y_sm, float* part,
+                                          int64_t part_elems, int64_t splits, int32_t dtype,
+                                          int32_t sdtype, void* stream) {
+  const char* what = "w8a16_gemm_residual";
+  GemmArgs a;
+  int32_t rc = gemm_setup(what, x, w, scales, y, m, n, k, x_sm, w_sn, s_sn, y_sm, a);
+  if (rc != MI_OK) return rc;
+  if (res == nullptr || res_sm < n) {
+    set_last_error("%s: null residual or residual rows shorter than N", what);
+    return MI_ERR_INVALID;
+  }
+  if (!dtypes_ok(dtype, sdtype)) {
+    set_last_error("%s: activations must be bf16 or fp16 (dtype %d, scales %d)", what,
+                   (int)dtype, (int)sdtype);
+    return MI_ERR_UNSUPPORTED;
+  }
+  a.res = res;
+  a.res_sm = res_sm;
+  a.res_line = ((uintptr_t)res % 16 == 0 && res_sm % 8 == 0) ? 1 : 0;
+  hipStream_t st = (hipStream_t)stream;
+  if (splits <= 1) {
+    launch_gemm<false>(a, 1, dtype, sdtype, st);
+    return launch_status(what);
+  }
+  const int64_t nk = k / kGmBK;
+  if (splits > nk || splits > 64) {
+    set_last_error("%s: need splits <= min(K / %d, 64) (splits=%lld)", what, kGmBK,
+                   (long long)splits);
+    return MI_ERR_INVALID;
+  }
+  const int64_t per = (nk + splits - 1) / splits;
+  const int64_t used = (nk + per - 1) / per;
+  if (part == nullptr || part_elems < used * m * n) {
+    set_last_error("%s: workspace needs %lld fp32 elements (given %lld)", what,
+                   (long long)(used * m * n), (long long)part_elems);
+    return MI_ERR_INVALID;
+  }
+  a.part = part;
+  a.split_stages = (int32_t)per;
+  a.part_vec = ((uintptr_t)part % 16 == 0 && n % 4 == 0) ? 1 : 0;
+  launch_gemm<true>(a, (int32_t)used, dtype, sdtype, st);
+  rc = launch_status(what);
+  if (rc != MI_OK) return rc;
+  launch_reduce(a, (int32_t)used, dtype, sdtype, st);
   return launch_status(what);
 }

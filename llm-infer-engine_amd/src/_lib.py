@@ -160,6 +160,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i64, _i64, _i64, _i64, _i64, _i64,    # x_sm w1_sn s1_sn w3_sn s3_sn y_sm
         _i32, _i32, _ptr,                      # dtype sdtype stream
     ]),
+    "mi_w8a16_gemm_residual": (_i32, [
+        _ptr, _ptr, _ptr, _ptr, _ptr,          # x w scales res y
+        _i64, _i64, _i64,                      # M N K
+        _i64, _i64, _i64, _i64, _i64,          # x_sm w_sn s_sn res_sm y_sm
+        _ptr, _i64, _i64,                      # part part_elems splits
+        _i32, _i32, _ptr,                      # dtype sdtype stream
+    ]),
     "mi_w8a16_linear_fused": (_i32, [
         _ptr, _i64, _ptr, _f32,                # x x_sm norm_w eps
         _ptr, _ptr, _i64,                      # w_a s_a w_sn_a

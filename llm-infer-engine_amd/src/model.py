@@ -43,11 +43,17 @@ class FeedForward(nn.Module):
         self.w2 = linear(hidden_dim, dim, bias=False)
         self.w3 = linear(dim, hidden_dim, bias=False)
 
-    def forward(self, x):
+    def forward(self, x, *, residual=None):
+        """w2(silu(w1(x)) * w3(x)) (src/model.py:21-25); with ``residual``
+        (keyword-only extension) residual + that, the block's add."""
         torch.cuda.nvtx.range_push("FFN")
-        out = self.w2(torch.nn.functional.silu(self.w1(x)) * self.w3(x))
+        out = self.down(torch.nn.functional.silu(self.w1(x)) * self.w3(x), residual)
         torch.cuda.nvtx.range_pop()
         return out
+
+    def down(self, h, residual=None):
+        out = self.w2(h)
+        return out if residual is None else residual + out
 
 
 class Attention(nn.Module):
@@ -65,9 +71,13 @@ class Attention(nn.Module):
         """The three input projections (src/model.py:54)."""
         return self.wq(x), self.wk(x), self.wv(x)
 
+    def out_proj(self, output, residual=None):
+        out = self.wo(output)
+        return out if residual is None else residual + out
+
     def forward(self, x, rope_cos, rope_sin, layer_idx=None, start_pos=0, kv_cache=None,
                 use_cuda_graph=False, scatter_positions=None, decode_attn_mask=None, *,
-                seq_lens=None, rope_by_position=False):
+                seq_lens=None, rope_by_position=False, residual=None):
         batch_size, query_len, _ = x.shape
         torch.cuda.nvtx.range_push("QKV_proj")
         xq, xk, xv = self.qkv(x)
@@ -106,7 +116,7 @@ class Attention(nn.Module):
 
         torch.cuda.nvtx.range_push("Output_proj")
         output = output.transpose(1, 2).contiguous().view(batch_size, query_len, -1)
-        out = self.wo(output)
+        out = self.out_proj(output, residual)
         torch.cuda.nvtx.range_pop()
         return out
 
@@ -122,13 +132,15 @@ class TransformerBlock(nn.Module):
     def forward(self, x, rope_cos, rope_sin, layer_idx=None, start_pos=0, kv_cache=None,
                 use_cuda_graph=False, scatter_positions=None, decode_attn_mask=None, **ext):
         torch.cuda.nvtx.range_push(f"Attn_{layer_idx}")
-        x = x + self.attention(self.attention_norm(x), rope_cos, rope_sin, layer_idx=layer_idx,
-                               start_pos=start_pos, kv_cache=kv_cache,
-                               use_cuda_graph=use_cuda_graph, scatter_positions=scatter_positions,
-                               decode_attn_mask=decode_attn_mask, **ext)
+        # x + attention(...) and x + feed_forward(...) (src/model.py:113-127), the
+        # adds passed down so a W8A16 projection can fuse them into its epilogue
+        x = self.attention(self.attention_norm(x), rope_cos, rope_sin, layer_idx=layer_idx,
+                           start_pos=start_pos, kv_cache=kv_cache,
+                           use_cuda_graph=use_cuda_graph, scatter_positions=scatter_positions,
+                           decode_attn_mask=decode_attn_mask, residual=x, **ext)
         torch.cuda.nvtx.range_pop()
         torch.cuda.nvtx.range_push(f"FFN_{layer_idx}")
-        x = x + self.feed_forward(self.ffn_norm(x))
+        x = self.feed_forward(self.ffn_norm(x), residual=x)
         torch.cuda.nvtx.range_pop()
         return x
 

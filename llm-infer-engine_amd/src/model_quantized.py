@@ -27,24 +27,42 @@ class QuantizedFeedForward(FeedForward):
     def __init__(self, dim: int, hidden_dim: int):
         super().__init__(dim, hidden_dim, W8A16Linear)
 
-    def forward(self, x):
+    def forward(self, x, *, residual=None):
         """Prefill-sized inputs: silu(w1(x)) * w3(x) in one GEMM launch (the
         same rounding points, neither projection written out) when its tiles
         fill the GPU; otherwise the op chain of src/model.py:23."""
         x2 = x.reshape(-1, x.shape[-1])
         w1, w3 = self.w1, self.w3
         if not quant_linear.swiglu_worth(x2.shape[0], x2.shape[1], w1.out_features, x.device):
-            return super().forward(x)
+            return super().forward(x, residual=residual)
         torch.cuda.nvtx.range_push("FFN")
         h = quant_linear.w8a16_gemm_swiglu(x2, w1.weight, w1.scales, w3.weight, w3.scales)
-        out = self.w2(h.view(*x.shape[:-1], w1.out_features))
+        out = self.down(h.view(*x.shape[:-1], w1.out_features), residual)
         torch.cuda.nvtx.range_pop()
         return out
+
+    def down(self, h, residual=None):
+        return _project_residual(self.w2, h, residual)
+
+
+def _project_residual(lin, h, residual):
+    """lin(h) + residual with the add in the GEMM epilogue at GEMM sizes (the
+    same roundings as the separate ops); otherwise the two ops."""
+    h2 = h.reshape(-1, h.shape[-1])
+    if residual is None or not quant_linear.gemm_supported(h2.shape[0], h2.shape[1]):
+        out = lin(h)
+        return out if residual is None else residual + out
+    res2 = residual.reshape(-1, lin.out_features)
+    y = quant_linear.w8a16_gemm_residual(h2, lin.weight, lin.scales, res2)
+    return y.view(*h.shape[:-1], lin.out_features)
 
 
 class QuantizedAttention(Attention):
     def __init__(self, args):
         super().__init__(args, W8A16Linear)
+
+    def out_proj(self, output, residual=None):
+        return _project_residual(self.wo, output, residual)
 
     def qkv(self, x):
         """Prefill-sized inputs: wq, wk and wv in one GEMM launch (bitwise the

@@ -144,6 +144,33 @@ def w8a16_gemm_mfma(x, weight, scales, *, splits: int | None = None):
 _GEMM_TILE_M, _GEMM_TILE_N = 128, 256
 
 
+def w8a16_gemm_residual(x, weight, scales, res, *, splits: int | None = None):
+    """res + w8a16(x, weight, scales) with the add in the GEMM epilogue (the
+    same roundings as the separate ops): x [M, K], res [M, N] in x's dtype.
+    The split rule is w8a16_gemm_mfma's."""
+    x, w, s = _prep(x, weight, scales)
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    M, K = x.shape
+    N = w.shape[0]
+    if res.shape != (M, N) or res.dtype != x.dtype or res.device != x.device:
+        raise ValueError(f"residual must be [{M}, {N}] {x.dtype} on {x.device}, "
+                         f"got {tuple(res.shape)} {res.dtype}")
+    if res.stride(1) != 1:
+        res = res.contiguous()
+    lib = _lib.load()
+    out = torch.empty((M, N), device=x.device, dtype=x.dtype)
+    S = lib.mi_w8a16_gemm_splits(M, N, K) if splits is None else int(splits)
+    part = torch.empty(S * M * N, device=x.device, dtype=torch.float32) if S > 1 else None
+    st = lib.mi_w8a16_gemm_residual(
+        x.data_ptr(), w.data_ptr(), s.data_ptr(), res.data_ptr(), out.data_ptr(), M, N, K,
+        x.stride(0), w.stride(0), s.stride(0), res.stride(0), out.stride(0),
+        _lib.ptr(part), 0 if part is None else part.numel(), S,
+        _lib.dtype_code(x.dtype), _lib.dtype_code(s.dtype), _lib.stream_of(x))
+    _lib.check(st, "w8a16_gemm_residual")
+    return out
+
+
 def gemm_multi_worth(M: int, K: int, out_features, device) -> bool:
     """Whether one mi_w8a16_gemm_multi launch should serve several projections
     of the same [M, K] input: the GEMM kernels apply and the 128 x 256 tiles of

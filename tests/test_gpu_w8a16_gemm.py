@@ -304,3 +304,26 @@ def test_quantized_feed_forward_fuses_at_prefill_sizes(dev):
     small = x[:1, :40]
     assert not swiglu_worth(40, 2048, 8192, dev)
     assert torch.equal(ff(small), FeedForward.forward(ff, small))
+
+
+@pytest.mark.parametrize("M,K,N,dtype,splits,pad", [(8192, 2048, 2048, torch.bfloat16, 1, 0),
+                                                    (300, 1024, 1000, torch.float16, 1, 4),
+                                                    (64, 8192, 2048, torch.bfloat16, None, 0),
+                                                    (100, 512, 256, torch.bfloat16, 4, 4)])
+def test_gemm_residual_is_the_separate_add(dev, M, K, N, dtype, splits, pad):
+    """res + w8a16(x) with the add in the epilogue, bitwise the GEMM (same
+    split count) followed by a separate add; 16-byte residual rows take the
+    whole-line path, padded ones (row stride N + 4) the 8-byte one; split-K
+    adds the residual in its reduce launch."""
+    from src import _lib
+    from src.quant_linear import w8a16_gemm_mfma, w8a16_gemm_residual
+    q, s = _quantised(N, K, dtype, dev, 100)
+    x = _x(M, K, dtype, dev, 101)
+    res = _x(M, N + pad, dtype, dev, 102)[:, :N]
+    S = _lib.load().mi_w8a16_gemm_splits(M, N, K) if splits is None else splits
+    if splits is None:
+        assert S > 1
+    y = w8a16_gemm_residual(x, q, s, res, splits=S)
+    assert torch.equal(y, res + w8a16_gemm_mfma(x, q, s, splits=S))
+    with pytest.raises(ValueError):
+        w8a16_gemm_residual(x, q, s, res[:, :-1])
