@@ -252,12 +252,13 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
     count (M = 4 x 2048), back to back, through the model's GEMM dispatch: wq,
     wk and wv in one mi_w8a16_gemm_multi launch (QuantizedAttention.qkv), w1 and
     w3 with the SwiGLU gating in one mi_w8a16_gemm_swiglu launch
-    (QuantizedFeedForward), wo and w2 through w8a16_gemm_mfma (the split-K form
-    where the tile grid leaves CUs idle).  per_projection also times each
-    projection on its own."""
+    (QuantizedFeedForward), wo and w2 with the block's residual add in their
+    epilogue (w8a16_gemm_residual).  per_projection also times each projection
+    on its own (w8a16_gemm_mfma, the split-K form where the tile grid leaves
+    CUs idle)."""
     from src import _lib
     from src.quant_linear import (gemm_multi_worth, swiglu_worth, w8a16_gemm_mfma,
-                                  w8a16_gemm_multi, w8a16_gemm_swiglu)
+                                  w8a16_gemm_multi, w8a16_gemm_residual, w8a16_gemm_swiglu)
     dev = torch.device("cuda:0")
     _lib.load()
     M = 4 * 2048
@@ -293,11 +294,17 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
         else:
             ffn_chain()
 
+    res = torch.randn(M, 2048, generator=g).to(torch.bfloat16).to(dev)
+
+    def call_res(i):
+        _, N, K = shapes[i]
+        w8a16_gemm_residual(xs[K], ws[i], ss[i], res)
+
     def step():
         qkv()
-        call(3)
+        call_res(3)
         ffn_in()
-        call(6)
+        call_res(6)
 
     def timed(fn, n):
         _settle(torch, fn, warmup)
@@ -325,11 +332,14 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
                           "tflops": round(2.0 * M * 16384 * 2048 / (t * 1e-3) / 1e12, 1)}
     t = timed(ffn_chain, steps)
     per["silu(w1)*w3 as separate ops"] = {"us": round(t * 1e3, 2)}
+    for i, name in ((3, "wo+residual"), (6, "w2+residual")):
+        per[name] = {"us": round(timed(lambda: call_res(i), steps) * 1e3, 2)}
     tf = flops / (ms * 1e-3) / 1e12
     # the dominant shape (w1/w3: 2 of the 7 calls, 54 % of the flops)
     dom = per["w1"]
     out = {"config": "W8A16 prefill projections of one Llama-3.2-1B layer as the model runs "
-                     "them (wq|wk|wv one launch, silu(w1)*w3 one launch, wo, w2), M = 8192 "
+                     "them (wq|wk|wv one launch, silu(w1)*w3 one launch, wo and w2 with the residual "
+                     "add in the epilogue), M = 8192 "
                      "tokens (config 2's B4 x S2048), bf16 activations, int8 weights, bf16 scales",
            "value": round(tf, 1), "unit": "TFLOP/s", "ms_per_step": round(ms, 4),
            "flops_per_step": flops, "per_projection": per,
@@ -337,7 +347,7 @@ def bench_w8a16_prefill(torch, steps: int, warmup: int) -> dict:
                         "achieved": dom["tflops"], "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": round(dom["tflops"] / BF16_PEAK_TFLOPS, 4),
                         "traffic": _traffic("w8a16_gemm_traffic.md", "hbm_bytes_per_launch_w1")}}
-    del xs, ws, ss
+    del xs, ws, ss, res
     torch.cuda.empty_cache()
     return out
 
