@@ -142,6 +142,16 @@ def w8a16_gemm_mfma(x, weight, scales, *, splits: int | None = None):
 
 
 _GEMM_TILE_M, _GEMM_TILE_N = 128, 256
+_CUS: dict = {}
+
+
+def _cu_count(device) -> int:
+    """Compute units of `device` (looked up once per device)."""
+    idx = torch.device(device).index
+    idx = torch.cuda.current_device() if idx is None else idx
+    if idx not in _CUS:
+        _CUS[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _CUS[idx]
 
 
 def w8a16_gemm_residual(x, weight, scales, res, *, splits: int | None = None):
@@ -179,7 +189,7 @@ def gemm_multi_worth(M: int, K: int, out_features, device) -> bool:
     if not gemm_supported(M, K):
         return False
     tiles = -(-M // _GEMM_TILE_M) * sum(-(-n // _GEMM_TILE_N) for n in out_features)
-    return tiles >= torch.cuda.get_device_properties(device).multi_processor_count
+    return tiles >= _cu_count(device)
 
 
 def w8a16_gemm_multi(x, mats):
@@ -226,7 +236,7 @@ def swiglu_worth(M: int, K: int, N: int, device) -> bool:
     if not gemm_supported(M, K):
         return False
     tiles = -(-M // _GEMM_TILE_M) * -(-N // (_GEMM_TILE_N // 2))
-    return tiles >= torch.cuda.get_device_properties(device).multi_processor_count
+    return tiles >= _cu_count(device)
 
 
 def w8a16_gemm_swiglu(x, w1, s1, w3, s3):
