@@ -292,3 +292,85 @@ def test_w8a16_linear_fused_c_side_validation(over, code, msg):
     lib = _lib.load()
     assert _fused_call(lib, **over) == code
     assert msg in _lib.last_error()
+
+
+def _multi_call(lib, n_mats=3, **over):
+    a = dict(x=1 << 20, m=300, k=2048, x_sm=2048, dtype=0, sdtype=0,
+             w=[1 << 21, 1 << 22, 1 << 23], s=[1 << 24, 1 << 25, 1 << 26],
+             y=[1 << 27, 1 << 28, 1 << 29], n=[2048, 512, 512], w_sn=[2048] * 3,
+             s_sn=[1] * 3, y_sm=[2048, 512, 512])
+    a.update(over)
+    P, I = ctypes.c_void_p * 4, ctypes.c_int64 * 4
+    arr = {key: (P if key in ("w", "s", "y") else I)(*(a[key] + [0] * (4 - len(a[key]))))
+           for key in ("w", "s", "y", "n", "w_sn", "s_sn", "y_sm")}
+    return lib.mi_w8a16_gemm_multi(a["x"], a["m"], a["k"], a["x_sm"], n_mats,
+                                   *[ctypes.addressof(arr[key]) for key in
+                                     ("w", "s", "y", "n", "w_sn", "s_sn", "y_sm")],
+                                   a["dtype"], a["sdtype"], None)
+
+
+@pytest.mark.parametrize("n_mats,over,code,msg", [
+    (0, {}, -1, "matrices"),
+    (5, {}, -1, "matrices"),
+    (3, {"w": [1 << 21, 0, 1 << 23]}, -1, "null"),
+    (3, {"k": 1000, "x_sm": 1000, "w_sn": [1008] * 3}, -2, "multiple of 64"),
+    (3, {"y_sm": [2048, 511, 512]}, -1, "strides"),
+    (3, {"dtype": 2}, -2, "bf16 or fp16"),
+])
+def test_w8a16_gemm_multi_c_side_validation(n_mats, over, code, msg):
+    """Every matrix is checked (and the count bounded) before any launch."""
+    from src import _lib
+    lib = _lib.load()
+    assert _multi_call(lib, n_mats, **over) == code
+    assert msg in _lib.last_error()
+
+
+def _swiglu_call(lib, **over):
+    a = dict(x=1 << 20, w1=1 << 21, s1=1 << 22, w3=1 << 23, s3=1 << 24, y=1 << 25, m=300,
+             n=1000, k=2048, x_sm=2048, w1_sn=2048, s1_sn=1, w3_sn=2048, s3_sn=1, y_sm=1000,
+             dtype=0, sdtype=0)
+    a.update(over)
+    return lib.mi_w8a16_gemm_swiglu(a["x"], a["w1"], a["s1"], a["w3"], a["s3"], a["y"], a["m"],
+                                    a["n"], a["k"], a["x_sm"], a["w1_sn"], a["s1_sn"],
+                                    a["w3_sn"], a["s3_sn"], a["y_sm"], a["dtype"], a["sdtype"],
+                                    None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    ({"w3": None}, -1, "null"),
+    ({"w3_sn": 2040}, -1, "w3 rows"),
+    ({"w3": (1 << 23) + 8}, -1, "w3 rows"),
+    ({"k": 1000, "x_sm": 1000, "w1_sn": 1008, "w3_sn": 1008}, -2, "multiple of 64"),
+    ({"dtype": 2}, -2, "bf16 or fp16"),
+])
+def test_w8a16_gemm_swiglu_c_side_validation(over, code, msg):
+    from src import _lib
+    lib = _lib.load()
+    assert _swiglu_call(lib, **over) == code
+    assert msg in _lib.last_error()
+
+
+def _residual_call(lib, **over):
+    a = dict(x=1 << 20, w=1 << 21, s=1 << 22, res=1 << 23, y=1 << 24, m=300, n=1000, k=2048,
+             x_sm=2048, w_sn=2048, s_sn=1, res_sm=1000, y_sm=1000, part=1 << 25,
+             part_elems=8 * 300 * 1000, splits=8, dtype=0, sdtype=0)
+    a.update(over)
+    return lib.mi_w8a16_gemm_residual(a["x"], a["w"], a["s"], a["res"], a["y"], a["m"], a["n"],
+                                      a["k"], a["x_sm"], a["w_sn"], a["s_sn"], a["res_sm"],
+                                      a["y_sm"], a["part"], a["part_elems"], a["splits"],
+                                      a["dtype"], a["sdtype"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    ({"res": None}, -1, "residual"),
+    ({"res_sm": 999}, -1, "residual"),
+    ({"splits": 33}, -1, "splits"),               # K / 64 = 32 stages
+    ({"part": None}, -1, "workspace"),
+    ({"part_elems": 8 * 300 * 1000 - 1}, -1, "workspace"),
+    ({"dtype": 2}, -2, "bf16 or fp16"),
+])
+def test_w8a16_gemm_residual_c_side_validation(over, code, msg):
+    from src import _lib
+    lib = _lib.load()
+    assert _residual_call(lib, **over) == code
+    assert msg in _lib.last_error()
