@@ -1,11 +1,12 @@
 """Fused W8A16 decode-step ops (one token per row, up to 16 rows).
 
 A decode step of the W8A16 block (src/model_quantized.py:42-93, the block
-composition of src/model.py:93-127) runs here in five launches per layer
+composition of src/model.py:93-127) runs here in six launches per layer
 instead of one per reference op:
 
   qkv_rope_append   rmsnorm -> wq|wk|wv -> RoPE(q); RoPE(k), v -> KV cache
-  flash_decode      split-KV attention over the cache (src/flash_decode.py)
+  flash_decode      split-KV attention over the cache and its LSE combine
+                    (two launches, src/flash_decode.py)
   linear_fused      wo + residual;  rmsnorm -> w1|w3 -> silu*mul;  w2 + residual
 
 Every value is rounded where the reference's separate ops round it (see

@@ -7,7 +7,7 @@ random-init model of the W8A16 decode benchmark: bf16 master weights drawn on
 the device, quantised with quantize_weight_symmetric_per_channel.
 
 Single-token decode (query length 1, up to 16 rows) runs each block through
-the fused decode-layer kernels (src/decode_layer.py): five launches per layer
+the fused decode-layer kernels (src/decode_layer.py): six launches per layer
 with the same rounding points as the op-by-op composition, which remains the
 path for prefill and for shapes the fused kernels do not take.
 """
