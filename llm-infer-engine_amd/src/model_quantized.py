@@ -8,8 +8,11 @@ the device, quantised with quantize_weight_symmetric_per_channel.
 
 Single-token decode (query length 1, up to 16 rows) runs each block through
 the fused decode-layer kernels (src/decode_layer.py): six launches per layer
-with the same rounding points as the op-by-op composition, which remains the
-path for prefill and for shapes the fused kernels do not take.
+with the same rounding points as the op-by-op composition.  Prefill-sized
+inputs keep the composition but fuse its GEMMs: wq|wk|wv in one launch
+(QuantizedAttention.qkv), silu(w1(x)) * w3(x) in one launch
+(QuantizedFeedForward), and the block's residual adds in the wo / w2
+epilogues; other shapes run op by op.
 """
 from __future__ import annotations
 
