@@ -212,8 +212,8 @@ int32_t mi_rope_kv_append(const void* xk, const void* xv, const void* cos,
  * query row i attends keys 0..i), out like q, lse [batch, n_heads, seq_len]
  * fp32 (natural log of the scaled scores) or NULL.  Unit head-dim stride,
  * 16-byte aligned rows.  head_dim 16, 32, 64, 128 or 256 (any power of two
- * the reference kernel's tl.dot takes): bf16/fp16 at 32, 64 and 128 run on
- * MFMA, the other head dims and fp32 on a VALU kernel in fp32 arithmetic.
+ * the reference kernel's tl.dot takes): bf16/fp16 at 32 to 256 run on MFMA,
+ * head_dim 16 and fp32 on a VALU kernel in fp32 arithmetic.
  * Query head h reads kv head h / (n_heads / n_kv_heads).
  * Replaces flash_attention_kernel + flash_attention
  *   src/flash_attn.py:5-83, src/flash_attn.py:85-111.

@@ -164,9 +164,14 @@ __device__ inline uint2 lds_read_tr(const unsigned char* p) {
 // of one block runs while the other's MFMAs execute).
 template <int D>
 constexpr int prefill_row_blocks() { return D == 64 ? 2 : 1; }  // D=128: registers
+// Blocks per CU the registers are sized for: at D = 256 one block (a wave then
+// holds its 32 x 256 fp32 O tile and the tile's K operands in 512 registers)
+// and its double-buffered K/V tiles take 128 KB of LDS.
+template <int D>
+constexpr int prefill_min_blocks() { return D >= 256 ? 1 : 2; }
 
 template <typename T, int D>
-__global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(256, prefill_min_blocks<D>()) void prefill_kernel(PrefillArgs a) {
   using MM = Mfma<T>;
   typedef typename MM::v8 v8;
   constexpr int BN = 64, KCH = D / 8, DC = D / 16, DB = D / 32, RB = prefill_row_blocks<D>();
@@ -316,20 +321,26 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) s[rb][sb][i] = 0.f;
       // all K operands of the tile are read before the first MFMA so the LDS
-      // latency is paid once per tile, not once per k-step
-      v8 ka[2][DC];
+      // latency is paid once per tile, not once per k-step (at D = 256 one
+      // 32-key half at a time: the registers are not there for both)
+      constexpr int KH = D >= 256 ? 1 : 2;   // halves whose K operands are live at once
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
+      for (int s0 = 0; s0 < 2; s0 += KH) {
+        v8 ka[KH][DC];
 #pragma unroll
-        for (int c = 0; c < DC; ++c)
-          ka[sb][c] = __builtin_bit_cast(
-              v8, *reinterpret_cast<const u32x4*>(kl + k_rd[c] + sb * 32 * ROW_B));
+        for (int sh = 0; sh < KH; ++sh)
 #pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
+          for (int c = 0; c < DC; ++c)
+            ka[sh][c] = __builtin_bit_cast(
+                v8, *reinterpret_cast<const u32x4*>(kl + k_rd[c] + (s0 + sh) * 32 * ROW_B));
 #pragma unroll
-        for (int c = 0; c < DC; ++c)
+        for (int sh = 0; sh < KH; ++sh)
 #pragma unroll
-          for (int rb = 0; rb < RB; ++rb) s[rb][sb] = MM::mma(ka[sb][c], qreg[rb][c], s[rb][sb]);
+          for (int c = 0; c < DC; ++c)
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+              s[rb][s0 + sh] = MM::mma(ka[sh][c], qreg[rb][c], s[rb][s0 + sh]);
+      }
       // V^T operands of the PV product.  At D = 64 they are read here, so
       // their latency hides under the softmax; at D = 128 the registers are
       // not there and they are read next to their MFMAs.
@@ -1089,7 +1100,13 @@ hipError_t launch(const PrefillArgs& a, int nwaves, hipStream_t stream) {
   const int n_pairs = a.B * a.Hkv * a.head_chunks;
   dim3 grid((unsigned)(n_pairs * a.n_pb));
   dim3 block((unsigned)(nwaves * 64));
-  const size_t smem = 2 * 2 * 64 * D * sizeof(T);  // 2 buffers x (K + V) tiles
+  constexpr size_t smem = 2 * 2 * 64 * D * sizeof(T);  // 2 buffers x (K + V) tiles
+  if constexpr (smem > 65536) {  // above the default dynamic-LDS limit: raise it once
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&prefill_kernel<T, D>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (attr != hipSuccess) return attr;
+  }
   hipLaunchKernelGGL((prefill_kernel<T, D>), grid, block, smem, stream, a);
   return hipGetLastError();
 }
@@ -1221,16 +1238,18 @@ int32_t attn_prefill(const void* q, const void* k, const void* v, void* o, float
   }
   hipError_t e;
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == MI_DTYPE_F32 || head_dim == 16 || head_dim == 256) {
+  if (dtype == MI_DTYPE_F32 || head_dim == 16) {
     e = dtype == MI_DTYPE_F32   ? launch_valu<float>(a, head_dim, st)
         : dtype == MI_DTYPE_BF16 ? launch_valu<bf16_t>(a, head_dim, st)
                                  : launch_valu<f16_t>(a, head_dim, st);
   } else if (dtype == MI_DTYPE_BF16) {
     e = sp ? launch_sp<bf16_t>(a, st)
-           : head_dim == 32 ? launch<bf16_t, 32>(a, nwaves, st) : launch<bf16_t, 128>(a, nwaves, st);
+        : head_dim == 32 ? launch<bf16_t, 32>(a, nwaves, st)
+        : head_dim == 128 ? launch<bf16_t, 128>(a, nwaves, st) : launch<bf16_t, 256>(a, nwaves, st);
   } else {
     e = sp ? launch_sp<f16_t>(a, st)
-           : head_dim == 32 ? launch<f16_t, 32>(a, nwaves, st) : launch<f16_t, 128>(a, nwaves, st);
+        : head_dim == 32 ? launch<f16_t, 32>(a, nwaves, st)
+        : head_dim == 128 ? launch<f16_t, 128>(a, nwaves, st) : launch<f16_t, 256>(a, nwaves, st);
   }
   if (e != hipSuccess) {
     set_last_error("attn_prefill: launch failed: %s", hipGetErrorString(e));

@@ -15,8 +15,8 @@ once in LDS for all query heads of a group.  Keyword-only extensions:
               in q's dtype the rotation runs in the attention kernel's Q prologue
               (one launch, q never rewritten); otherwise apply_rotary runs first.
 head_dim 16, 32, 64, 128 or 256 (src/flash_attn.py:29-32 takes any power of
-two): bf16/fp16 at 32, 64 and 128 run on MFMA, the other head dims and fp32 on
-a VALU kernel in fp32 arithmetic.
+two): bf16/fp16 at 32 to 256 run on MFMA, head_dim 16 and fp32 on a VALU
+kernel in fp32 arithmetic.
 """
 from __future__ import annotations
 

@@ -44,8 +44,8 @@ def test_prefill_matches_oracle(dev, dtype, D, Hq, Hkv, S):
 @pytest.mark.parametrize("Hq,Hkv,S", [(8, 2, 77), (16, 16, 256), (4, 1, 130)])
 def test_prefill_other_head_dims(dev, dtype, D, Hq, Hkv, S):
     """head_dim 16, 32 and 256 (the reference kernel takes any power-of-two
-    head_dim, src/flash_attn.py:29-32): bf16/fp16 at 32 on MFMA, the rest on
-    the VALU kernel; with q's RoPE fused and without."""
+    head_dim, src/flash_attn.py:29-32): bf16/fp16 at 32 and 256 on MFMA, 16
+    and fp32 on the VALU kernel; with q's RoPE fused and without."""
     from src.rope import apply_rotary
     B = 2
     q = randn((B, S, Hq, D), 80, dtype, dev).transpose(1, 2)
