@@ -557,6 +557,7 @@ __global__ __launch_bounds__(256) void decode_combine_wave_kernel(CombineArgs a)
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     float x = acc[i];
+    if (ncol <= 4) x += lane_xor<4>(x, lane);
     if (ncol <= 8) x += lane_xor<8>(x, lane);
     if (ncol <= 16) x += lane_xor<16>(x, lane);
     if (ncol <= 32) x += lane_xor<32>(x, lane);
@@ -718,8 +719,7 @@ HostGeom host_geom(int32_t dtype, int64_t D) {
 int gc_max(int32_t dtype, int64_t D) { return host_geom(dtype, D).gcmax; }
 
 bool supported_head_dim(int32_t dtype, int64_t D) {
-  if (dtype == MI_DTYPE_F32) return D == 32 || D == 64 || D == 128 || D == 256;
-  return D == 64 || D == 128 || D == 256 || D == 32;
+  return D == 16 || D == 32 || D == 64 || D == 128 || D == 256;
 }
 
 struct Plan {
@@ -790,6 +790,7 @@ template <typename T>
 hipError_t launch_split(const DecodeArgs& a, const Plan& p, int64_t B,
                         int64_t Hkv, int64_t D, hipStream_t stream) {
   switch (D) {
+    case 16: return launch_split_d<T, 16>(a, p, B, Hkv, stream);
     case 32: return launch_split_d<T, 32>(a, p, B, Hkv, stream);
     case 64: return launch_split_d<T, 64>(a, p, B, Hkv, stream);
     case 128: return launch_split_d<T, 128>(a, p, B, Hkv, stream);
@@ -822,7 +823,7 @@ int32_t check_common(const void* q, const void* k, const void* v,
     return MI_ERR_INVALID;
   }
   if (!supported_head_dim(dtype, D)) {
-    set_last_error("decode: head_dim %lld has no kernel (supported: 32, 64, 128, 256)",
+    set_last_error("decode: head_dim %lld has no kernel (supported: 16, 32, 64, 128, 256)",
                    (long long)D);
     return MI_ERR_UNSUPPORTED;
   }
@@ -1064,7 +1065,7 @@ extern "C" int32_t mi_decode_combine(const float* part_m, const float* part_l,
                    (long long)num_splits, (long long)kMaxSplits);
     return MI_ERR_UNSUPPORTED;
   }
-  if (head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256) {
+  if (head_dim != 16 && head_dim != 32 && head_dim != 64 && head_dim != 128 && head_dim != 256) {
     set_last_error("decode_combine: head_dim %lld unsupported", (long long)head_dim);
     return MI_ERR_UNSUPPORTED;
   }

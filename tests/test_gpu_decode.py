@@ -51,13 +51,22 @@ def test_split_count_invariance(dev, num_splits):
     assert max_abs(lse, ref_lse) < LSE_TOL
 
 
-@pytest.mark.parametrize("D", [32, 256])
-def test_decode_other_head_dims(dev, D):
-    q, k, v = _inputs(2, 6, 2, 515, D, torch.bfloat16, dev, seed=9)
-    out, lse = _fd()(q, k, v, return_lse=True)
-    ref, ref_lse = ora.decode(q, k, v)
-    assert max_abs(out, ref) < 2e-2
-    assert max_abs(lse, ref_lse) < LSE_TOL
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [16, 32, 256])
+def test_decode_other_head_dims(dev, D, dtype):
+    """head_dim 16 / 32 / 256 (the reference's decode takes any power of two up
+    to 256, src/flash_decode.py:276-277) through the default split count, a
+    single split (no combine), 40 splits (the block-per-row combine), per-
+    sequence lengths and a mask."""
+    q, k, v = _inputs(2, 6, 2, 515, D, dtype, dev, seed=9)
+    sl = torch.tensor([515, 77], dtype=torch.int64, device=dev)
+    mask = (torch.rand(2, 515, generator=torch.Generator().manual_seed(2)) < 0.5).to(dev)
+    for kw, ref_kw in (({}, {}), ({"num_splits": 1}, {}), ({"num_splits": 40}, {}),
+                       ({"seq_lens": sl}, {"seq_lens": sl}), ({"mask": mask}, {"mask": mask})):
+        out, lse = _fd()(q, k, v, return_lse=True, **kw)
+        ref, ref_lse = ora.decode(q, k, v, **ref_kw)
+        assert max_abs(out, ref) < TOL[dtype], (D, dtype, kw.keys())
+        assert max_abs(lse, ref_lse) < LSE_TOL, (D, dtype, kw.keys())
 
 
 @pytest.mark.parametrize("shape", ["1d", "2d", "4d", "4d_b1"])
