@@ -532,6 +532,87 @@ def cpu_baselines(torch) -> dict:
     return out
 
 
+def bench_prefill_d128(torch, steps: int, warmup: int) -> dict:
+    """Causal GQA prefill at the Llama-3.2-3B head shape of configs 3 and 4
+    (B4 S2048 24/8 heads D128, bf16, fp32 LSE): prefill_kernel<128>, one
+    launch per step, timed as the headline leg is."""
+    from src.flash_attn import flash_attention
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, S, D = 4, 24, 8, 2048, 128
+    g = torch.Generator("cpu").manual_seed(1)
+    q = torch.randn((B, Hq, S, D), generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn((B, Hkv, S, D), generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn((B, Hkv, S, D), generator=g).to(torch.bfloat16).to(dev)
+    flops = 4.0 * B * Hq * S * S * D / 2
+    step = lambda: flash_attention(q, k, v, return_lse=True)  # noqa: E731
+    _settle(torch, step, warmup)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    achieved = flops / (ms * 1e-3) / 1e12
+    return {"config": "causal GQA prefill B4 S2048 Hq24 Hkv8 D128 (the 3B head shape of configs "
+                      "3/4), bf16, fp32 LSE",
+            "value": round(achieved, 1), "unit": "TFLOP/s", "ms_per_step": ms, "flops": flops,
+            "roofline": {"bound": "mfma", "kernel": "prefill_kernel<128>",
+                         "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
+                         "traffic": _traffic("prefill_d128_traffic.md", "hbm_bytes_per_launch")}}
+
+
+def bench_w8a16_prefill_e2e(torch, steps: int, warmup: int) -> dict:
+    """The reference's timed prefill (main.py:233-243): the whole Llama-3.2-1B
+    random-init W8A16 model over a prompt, model(tokens, start_pos=0,
+    kv_cache=...), logits of the last position.  Batch 4 x 2048 tokens
+    (config 2's token count).  Work per call: the seven int8 projections of 16
+    layers (2 FLOP per weight and token), causal attention (4*B*Hq*S^2*D/2 per
+    layer) and the last rows' lm_head."""
+    from src.config import ModelArgs
+    from src.kv_cache import KVCache
+    from src.model_quantized import build_random_quantized
+    dev = torch.device("cuda:0")
+    B, S = 4, 2048
+    args = ModelArgs(max_batch_size=B, max_seq_len=S, device=str(dev))
+    model = build_random_quantized(args, seed=0, device=str(dev))
+    kv = KVCache(args, dtype=torch.bfloat16)
+    tokens = torch.randint(0, args.vocab_size, (B, S),
+                           generator=torch.Generator().manual_seed(0)).to(dev)
+    hd = args.dim // args.n_heads
+    kvd = args.n_kv_heads * hd
+    ffn = 8192
+    lin_params = args.n_layers * (2 * args.dim * args.dim + 2 * kvd * args.dim
+                                  + 3 * ffn * args.dim)
+    flops = (2.0 * B * S * lin_params
+             + args.n_layers * 4.0 * B * args.n_heads * S * S * hd / 2
+             + 2.0 * B * args.vocab_size * args.dim)
+
+    def step():
+        with torch.no_grad():
+            return model(tokens, start_pos=0, kv_cache=kv)
+    _settle(torch, step, max(2, warmup // 4), min_s=0.5)
+    n = max(5, steps // 2)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(n):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / n
+    out = {"config": "Llama-3.2-1B random-init W8A16 prefill, B4 x 2048 tokens, "
+                     "model(tokens, start_pos=0, kv_cache) (logits of the last position)",
+           "value": round(flops / (ms * 1e-3) / 1e12, 1), "unit": "TFLOP/s",
+           "ms_per_step": ms, "tokens_per_s": round(B * S / (ms * 1e-3), 1), "flops": flops,
+           "steps": n}
+    del model, kv
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_prefill_cfg1(torch, steps: int, warmup: int) -> dict:
     """Config 1 on the GPU (fp32 RoPE on Q and K + causal GQA prefill, B1 S512
     32/8 D64): the parity configuration, timed beside its CPU baseline."""
@@ -625,7 +706,8 @@ def main() -> None:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run one plain 1 GiB device copy (scales rocprofv3 FETCH/WRITE_SIZE)")
-    ap.add_argument("--only", choices=["prefill", "prefill_model", "decode", "step", "gemm", "load"],
+    ap.add_argument("--only", choices=["prefill", "prefill_model", "decode", "step", "gemm", "e2e",
+                                       "load"],
                     default=None,
                     help="run one leg only (profiling)")
     args = ap.parse_args()
@@ -652,6 +734,7 @@ def main() -> None:
     if args.only in (None, "prefill"):
         pre = bench_prefill(torch, args.steps, args.warmup)
         extra["prefill_config1"] = bench_prefill_cfg1(torch, args.steps, args.warmup)
+        extra["prefill_d128"] = bench_prefill_d128(torch, args.steps, args.warmup)
     if args.only in (None, "prefill_model"):
         extra["prefill_config2_model_layout"] = bench_prefill_model_layout(torch, args.steps,
                                                                            args.warmup)
@@ -662,6 +745,8 @@ def main() -> None:
         extra["decode_step_config5"] = bench_config5(torch, args.steps, args.warmup)
     if args.only in (None, "gemm"):
         extra["w8a16_prefill_gemm"] = bench_w8a16_prefill(torch, args.steps, args.warmup)
+    if args.only in (None, "e2e"):
+        extra["w8a16_prefill_model"] = bench_w8a16_prefill_e2e(torch, args.steps, args.warmup)
     if args.only == "load":    # host I/O; not part of the default run
         extra["checkpoint_load"] = bench_loader(torch)
     cpu = None

@@ -52,7 +52,10 @@ const char* mi_last_error(void);
  *
  * q        [batch, n_heads, 1, head_dim]      strides (q_sb, q_sh, q_sd)
  * k, v     [batch, n_kv_heads, kv_len, head_dim], innermost stride 1,
- *          rows 16-byte aligned                strides (*_sb, *_sh, *_sl)
+ *          element-aligned                     strides (*_sb, *_sh, *_sl)
+ * head_dim 1 to 256 (src/flash_decode.py:274-277).  Rows that are 16-byte
+ *          aligned are read with 128-bit loads (a head_dim that is not a
+ *          multiple of 16 bytes, or unaligned rows, use element loads).
  * mask     optional bool bytes; key j of batch b participates iff
  *          mask[b*mask_sb + j*mask_sl] != 0 (mask_sb = 0 broadcasts)
  *          (src/flash_decode.py:87-95, :215-233)
@@ -97,13 +100,29 @@ int32_t mi_decode_combine(const float* part_m, const float* part_l,
  * Both decode phases in one call (what flash_decode / decode_attention use).
  * With num_splits == 1 the partial buffers may be NULL: the split kernel then
  * normalises and writes out/lse itself (single launch).
+ * arrive   optional uint64 [batch * n_heads] arrival counters (e.g. from
+ *          mi_decode_arrive_counters; batch * n_heads <= MI_DECODE_ARRIVE_SLAB
+ *          for one of its slabs): all zero before the first call, and every
+ *          call leaves them zero.  Calls that share one counter array must not
+ *          overlap in time (issue them on one stream).  With counters, a call
+ *          whose split blocks are few and short (no mask, a power-of-two
+ *          head_dim, 2..16 splits, at most one block per compute unit) runs the
+ *          LSE combine inside the split launch: the splits of each (batch,
+ *          kv-head) group are dealt to one XCD and the last of them to finish
+ *          combines the group's partials from that XCD's L2 -- one launch
+ *          instead of two, the same bits as the wave combine kernel.  Other
+ *          calls, and NULL, run two launches.  A group whose splits did not all
+ *          run on one XCD (never on a device that deals workgroups
+ *          round-robin, as gfx950 does) yields NaN outputs and lse instead of
+ *          a result.
  * Replaces flash_decode() src/flash_decode.py:236-370 and
  * decode_attention() src/decode_attn.py:137-166.
  */
 int32_t mi_flash_decode(const void* q, const void* k, const void* v,
                         const uint8_t* mask, int64_t mask_sb, int64_t mask_sl,
                         const int64_t* seq_lens, float* part_m, float* part_l,
-                        float* part_acc, void* out, float* lse, int64_t batch,
+                        float* part_acc, uint64_t* arrive, void* out, float* lse,
+                        int64_t batch,
                         int64_t n_heads, int64_t n_kv_heads, int64_t kv_len,
                         int64_t head_dim, int64_t num_splits, int64_t q_sb,
                         int64_t q_sh, int64_t q_sd, int64_t k_sb, int64_t k_sh,
@@ -113,6 +132,21 @@ int32_t mi_flash_decode(const void* q, const void* k, const void* v,
                         void* stream);
 
 /*
+ * Arrival counters for mi_flash_decode's `arrive`, owned by the library:
+ * *counters = a slab of MI_DECODE_ARRIVE_SLAB zeroed uint64 counters of the
+ * current device reserved for `stream` (the same slab on every call with that
+ * stream; calls on one stream never overlap, so they may share it).  The slabs
+ * are part of the library's code object (no allocation); once
+ * MI_DECODE_ARRIVE_SLABS streams of a device hold one, further streams get
+ * MI_ERR_UNSUPPORTED (pass NULL: two launches).  A graph captured on a stream
+ * keeps that stream's slab: replay it on that stream, or while no other call
+ * runs on it.  No counterpart in the reference.
+ */
+#define MI_DECODE_ARRIVE_SLAB 8192
+#define MI_DECODE_ARRIVE_SLABS 32
+int32_t mi_decode_arrive_counters(void* stream, uint64_t** counters);
+
+/*
  * mi_flash_decode without a caller workspace: the same kernels, with the split
  * partials kept in a library-owned device array of
  * MI_DECODE_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends).  It
@@ -120,7 +154,10 @@ int32_t mi_flash_decode(const void* q, const void* k, const void* v,
  * allocate (code under graph capture, serving loops that forbid allocation).
  * No counterpart in the reference.  The partials need
  * batch*n_heads*num_splits*(head_dim+2)*4 bytes (each array rounded up to 256
- * bytes); larger calls return MI_ERR_UNSUPPORTED before launching anything.
+ * bytes) of the array's first 16 MiB - 64 KiB; larger calls return
+ * MI_ERR_UNSUPPORTED before launching anything.  The last 64 KiB hold the
+ * arrival counters of the in-launch combine (batch * n_heads <= 8192; larger
+ * calls combine in a second launch).
  * Every call on one GPU shares that GPU's array: calls that overlap in time on
  * one device (different streams, or host threads) race and must not be issued.
  * num_splits == 1 uses no scratch.

@@ -31,6 +31,9 @@ constexpr float kNegBig = -1.0e30f;
 void set_last_error(const char* fmt, ...);
 // compute units of the current device (cached per device; 256 if unknown)
 int device_cu_count();
+// XCDs (XCCs) of the current device, over which the hardware deals workgroup
+// ids round-robin (cached per device; 1 if unknown)
+int device_xcc_count();
 
 // ---------------------------------------------------------- element traits
 template <typename T> struct Elem;

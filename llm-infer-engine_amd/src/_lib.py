@@ -60,6 +60,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _ptr, _i64, _i64,
         _ptr,
         _ptr, _ptr, _ptr,
+        _ptr,                                  # arrive (in-launch combine counters)
         _ptr, _ptr,                            # out lse
         _i64, _i64, _i64, _i64, _i64, _i64,
         _i64, _i64, _i64,
@@ -80,6 +81,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _i64, _i64, _i64,                      # o strides
         _f32, _i32, _i32, _ptr,                # sm_scale empty_nan dtype stream
     ]),
+    "mi_decode_arrive_counters": (_i32, [_ptr, _ptr]),      # stream, uint64_t** out
     "mi_decode_default_splits": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "mi_decode_effective_splits": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "mi_attn_prefill": (_i32, [
@@ -249,6 +251,27 @@ def ptr(t: torch.Tensor | None) -> int | None:
 def stream_of(t: torch.Tensor) -> int:
     """hipStream_t of torch's current stream on t's device (graph-capture aware)."""
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+_ARRIVE: dict[tuple[int, int], int | None] = {}
+ARRIVE_SLAB = 8192   # MI_DECODE_ARRIVE_SLAB
+
+
+def arrive_counters(t: torch.Tensor, n_groups: int) -> int | None:
+    """Device address of the library's zeroed arrival counters for torch's
+    current stream on t's device (mi_decode_arrive_counters; the in-launch LSE
+    combine of mi_flash_decode), or None when they cannot serve the call (more
+    than a slab's worth of groups, or every slab taken by other streams)."""
+    if n_groups > ARRIVE_SLAB:
+        return None
+    stream = stream_of(t)
+    key = (t.device.index if t.device.index is not None else torch.cuda.current_device(), stream)
+    if key not in _ARRIVE:
+        out = ctypes.c_void_p()
+        with torch.cuda.device(t.device):
+            st = load().mi_decode_arrive_counters(stream, ctypes.byref(out))
+        _ARRIVE[key] = out.value if st == MI_OK else None
+    return _ARRIVE[key]
 
 
 def require_device(t: torch.Tensor, what: str) -> None:

@@ -3,9 +3,10 @@
 ``flash_decode(q, k, v, mask=None)`` keeps the reference's signature, argument
 checks and error messages (src/flash_decode.py:215-285) and the same result:
 softmax over the keys j < L with mask[b, j] true, 0 for a row with no such key.
-The work runs in two HIP kernels (mi_flash_decode): a split kernel whose
+The work runs in one HIP launch (mi_flash_decode): a split kernel whose
 workgroups each stream one (batch, kv-head, key-range) ONCE for all query heads
-of the GQA group, and an LSE combine.  Keyword-only extensions:
+of the GQA group, and whose last workgroup of each group combines the group's
+partials (LSE combine) from its XCD's L2.  Keyword-only extensions:
   num_splits  key-range count (default: chosen from the CU count); there is no
               65,536-key cap as in the reference (src/flash_decode.py:278-279).
   seq_lens    int64 [B] device tensor; keys >= seq_lens[b] are never read
@@ -43,11 +44,10 @@ def _mask_strides(mask: torch.Tensor, batch_size: int, kv_len: int) -> tuple[int
 
 
 def _kv_ready(t: torch.Tensor) -> torch.Tensor:
-    """K/V rows must have unit innermost stride and 16-byte alignment for the
-    128-bit loads; other layouts are re-laid out once (a copy, not compute)."""
-    es = t.element_size()
-    if (t.stride(3) == 1 and t.data_ptr() % 16 == 0 and (t.stride(2) * es) % 16 == 0
-            and (t.stride(1) * es) % 16 == 0 and (t.stride(0) * es) % 16 == 0):
+    """K/V rows must have unit innermost stride (rows that are also 16-byte
+    aligned are read with 128-bit loads, others element by element); other
+    layouts are re-laid out once (a copy, not compute)."""
+    if t.stride(3) == 1 or t.shape[3] == 1:
         return t
     return t.contiguous()
 
@@ -91,10 +91,13 @@ def _run_decode(q, k, v, mask, seq_lens, num_splits, return_lse, empty_nan, what
     else:
         part_m = part_l = part_acc = None
     lib = _lib.load()
+    # with several splits the LSE combine runs inside the split launch, on the
+    # library's per-stream arrival counters (batch * n_heads bounds the groups)
+    arrive = _lib.arrive_counters(q, batch_size * n_heads) if num_splits > 1 else None
     st = lib.mi_flash_decode(
         q.data_ptr(), k.data_ptr(), v.data_ptr(),
         _lib.ptr(mask), mask_sb, mask_sl, _lib.ptr(seq_lens),
-        _lib.ptr(part_m), _lib.ptr(part_l), _lib.ptr(part_acc),
+        _lib.ptr(part_m), _lib.ptr(part_l), _lib.ptr(part_acc), arrive,
         out.data_ptr(), _lib.ptr(lse),
         batch_size, n_heads, n_kv_heads, kv_len, head_dim, num_splits,
         q.stride(0), q.stride(1), q.stride(3),

@@ -56,3 +56,42 @@ def should_quantize_key(model_key: str) -> bool:
     if len(parts) < 5 or parts[0] != "layers" or parts[-1] != "weight":
         return False
     return ".".join(parts[2:-1]) in get_transformer_linear_names()
+
+
+# Accuracy metrics comparing a W8A16 model's logits with its bf16 master (the
+# reference's evaluation scripts import them, src/quant_utils.py:39-96); plain
+# torch reductions, not on the hot path.
+
+def cosine_similarity(a: torch.Tensor, b: torch.Tensor, eps: float = 1e-12) -> torch.Tensor:
+    """Mean over rows (all leading dims) of cos(a_row, b_row), in fp32."""
+    a2 = a.reshape(-1, a.shape[-1]).float()
+    b2 = b.reshape(-1, b.shape[-1]).float()
+    dots = (a2 * b2).sum(dim=1)
+    norms = (a2.norm(dim=1) * b2.norm(dim=1)).clamp_min(eps)
+    return (dots / norms).mean()
+
+
+def logits_max_abs_error(a: torch.Tensor, b: torch.Tensor) -> float:
+    return float((a.float() - b.float()).abs().max())
+
+
+def logits_relative_error(a: torch.Tensor, b: torch.Tensor, eps: float = 1e-12) -> float:
+    """Mean of |a - b| / max(|a|, eps) over elements (a is the reference)."""
+    af = a.float()
+    return float(((af - b.float()).abs() / af.abs().clamp_min(eps)).mean())
+
+
+def top1_agreement(a: torch.Tensor, b: torch.Tensor) -> float:
+    """Fraction of positions whose argmax over the last dim agrees."""
+    return float((a.argmax(dim=-1) == b.argmax(dim=-1)).float().mean())
+
+
+def perplexity(logits: torch.Tensor, labels: torch.Tensor) -> float:
+    """exp(mean next-token cross entropy): logits[:, t] predicts labels[:, t+1];
+    [S, V] / [S] inputs are treated as one sequence; labels == -100 are ignored."""
+    if logits.dim() == 2:
+        logits, labels = logits[None], labels[None]
+    pred = logits[:, :-1, :].float().reshape(-1, logits.shape[-1])
+    tgt = labels[:, 1:].reshape(-1)
+    nll = torch.nn.functional.cross_entropy(pred, tgt, reduction="mean", ignore_index=-100)
+    return float(torch.exp(nll))

@@ -65,10 +65,11 @@ def _decode_call(lib, **over):
 @pytest.mark.parametrize("over,code,msg", [
     ({"q": None}, -1, "null"),
     ({"Hq": 12, "Hkv": 8}, -1, "divisible"),
-    ({"D": 96}, -2, "head_dim"),
+    ({"D": 257}, -2, "head_dim"),
+    ({"D": 0}, -1, "positive"),
     ({"dtype": 7}, -1, "dtype"),
     ({"L": 0}, -1, "positive"),
-    ({"k": (1 << 20) + 2}, -1, "aligned"),
+    ({"k": (1 << 20) + 1}, -1, "element size"),     # bf16 K at an odd byte address
     ({"pm": None}, -1, "partial"),
     ({"S": 100000}, -2, "num_splits"),
 ])
@@ -77,6 +78,26 @@ def test_c_side_validation(over, code, msg):
     lib = _lib.load()
     assert _decode_call(lib, **over) == code
     assert msg in _lib.last_error()
+
+
+@pytest.mark.parametrize("head_dim", [1, 4, 7, 0, -3, 300])
+def test_split_rules_at_any_head_dim(head_dim):
+    """The split-count helpers and the allocation-free entry point take any
+    head_dim without dividing by a zero lane count: head dims below one 16-byte
+    chunk (bf16 D < 8) get a valid count, and head dims outside 1..256 are
+    refused by the launch, not by a crash."""
+    from src import _lib
+    lib = _lib.load()
+    s = lib.mi_decode_effective_splits(1, 8, 2, 4096, head_dim, 2)
+    assert s >= 2
+    assert lib.mi_decode_default_splits(1, 8, 2, 4096, head_dim) >= 1
+    if 1 <= head_dim <= 256:
+        return          # a valid call would launch: not with these stand-in pointers
+    st = lib.mi_flash_decode_noalloc(1 << 20, 1 << 20, 1 << 20, None, 0, 0, None, 1 << 20, None,
+                                     1, 8, 2, 4096, head_dim, 2, 8, 8, 1,
+                                     *([1] * 6), 1, 1, 1, 0.1, 0, 0, None)
+    assert st in (-1, -2)
+    assert "head_dim" in _lib.last_error() or "positive" in _lib.last_error()
 
 
 def test_rope_kv_append_rejects_out_of_capacity():

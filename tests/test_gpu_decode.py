@@ -263,3 +263,126 @@ def test_seq_lens_rows_dealt_by_length(dev, B):
                          seq_lens=lens[perm].to(dev), num_splits=2, return_lse=True)
     assert torch.equal(out_p, out[pd])
     assert torch.equal(lse_p, lse[pd])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [8, 48, 80, 96, 112, 160, 192, 200])
+def test_decode_head_dims_not_powers_of_two(dev, D, dtype):
+    """Any head_dim <= 256 (the reference pads to the next power of two and
+    masks d < HEAD_DIM, src/flash_decode.py:55-61, :274-277): head dims that
+    fill whole 16-byte chunks run the chunk loads with the lanes past them
+    idle; through the default split count, one split, 40 splits, per-sequence
+    lengths and a mask."""
+    q, k, v = _inputs(2, 6, 2, 515, D, dtype, dev, seed=19)
+    sl = torch.tensor([515, 77], dtype=torch.int64, device=dev)
+    mask = (torch.rand(2, 515, generator=torch.Generator().manual_seed(5)) < 0.5).to(dev)
+    for kw, ref_kw in (({}, {}), ({"num_splits": 1}, {}), ({"num_splits": 40}, {}),
+                       ({"seq_lens": sl}, {"seq_lens": sl}), ({"mask": mask}, {"mask": mask}),
+                       ({"mask": mask, "num_splits": 3}, {"mask": mask})):
+        out, lse = _fd()(q, k, v, return_lse=True, **kw)
+        ref, ref_lse = ora.decode(q, k, v, **ref_kw)
+        assert out.shape == q.shape
+        assert max_abs(out, ref) < TOL[dtype], (D, dtype, kw.keys())
+        assert max_abs(lse, ref_lse) < LSE_TOL, (D, dtype, kw.keys())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("D", [1, 3, 4, 36, 100, 130, 255, 256])
+def test_decode_element_loads(dev, D, dtype):
+    """Head dims whose rows are not whole 16-byte chunks (and rows that are
+    not 16-byte aligned: a [..., 1:] view of wider rows) are read element by
+    element; D = 256 through such a view checks the same path at full width."""
+    B, Hq, Hkv, L = 3, 8, 2, 700
+    g = torch.Generator().manual_seed(D)
+    q = torch.randn((B, Hq, 1, D), generator=g).to(dtype).to(dev)
+    kw_ = torch.randn((B, Hkv, L, D + 1), generator=g).to(dtype).to(dev)
+    vw_ = torch.randn((B, Hkv, L, D + 1), generator=g).to(dtype).to(dev)
+    k, v = kw_[..., 1:], vw_[..., 1:]
+    sl = torch.tensor([700, 1, 333], dtype=torch.int64, device=dev)
+    for kw, ref_kw in (({}, {}), ({"num_splits": 1}, {}), ({"num_splits": 7}, {}),
+                       ({"seq_lens": sl}, {"seq_lens": sl})):
+        out, lse = _fd()(q, k, v, return_lse=True, **kw)
+        ref, ref_lse = ora.decode(q, k, v, **ref_kw)
+        assert max_abs(out, ref) < TOL[dtype], (D, dtype, kw.keys())
+        assert max_abs(lse, ref_lse) < LSE_TOL, (D, dtype, kw.keys())
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,L,D,S", [
+    (8, 32, 8, 4097, 64, 4),        # config 5's per-layer shape: in-launch combine
+    (2, 8, 2, 999, 128, 8),         # few groups, 8 splits: in-launch combine
+    (4, 8, 8, 5000, 128, 2),        # MHA, 2 splits widened to 4: in-launch combine
+    (16, 24, 8, 3000, 128, 4),      # config 3's heads, 512 blocks: two launches
+    (1, 24, 8, 20000, 128, 32),     # config 4-like, 32 splits: two launches
+    (3, 8, 2, 999, 96, 16),         # padded head_dim: two launches
+    (2, 6, 2, 2000, 64, 200),       # many splits: two launches (block combine)
+])
+def test_in_launch_combine_matches_combine_kernel(dev, monkeypatch, B, Hq, Hkv, L, D, S):
+    """With the library's arrival counters, calls whose split blocks are few
+    and short run the LSE combine inside the split launch (the last split of
+    each group combines); it gives bit for bit what the separate combine
+    kernel gives whenever that kernel is the wave-per-row one (<= 16 splits,
+    >= 64 rows), and the oracle's result otherwise; three calls in a row check
+    that every call leaves its arrival counters at zero.  Other shapes take
+    the two launches either way."""
+    from src import _lib
+    q, k, v = _inputs(B, Hq, Hkv, L, D, torch.bfloat16, dev, seed=31)
+    g = torch.Generator().manual_seed(S)
+    sl = torch.randint(1, L + 1, (B,), generator=g).to(dev)
+    ref, ref_lse = ora.decode(q, k, v, seq_lens=sl)
+    fused = [_fd()(q, k, v, num_splits=S, seq_lens=sl, return_lse=True) for _ in range(3)]
+    with monkeypatch.context() as m:
+        m.setattr(_lib, "arrive_counters", lambda *a: None)
+        two = _fd()(q, k, v, num_splits=S, seq_lens=sl, return_lse=True)
+    eff = int(_lib.load().mi_decode_effective_splits(B, Hq, Hkv, L, D, S))
+    for out, lse in fused:
+        assert torch.equal(out, fused[0][0]) and torch.equal(lse, fused[0][1])
+        assert max_abs(out, ref) < 2e-2
+        assert max_abs(lse, ref_lse) < LSE_TOL
+    if eff <= 16 and B * Hq >= 64:
+        assert torch.equal(fused[0][0], two[0]) and torch.equal(fused[0][1], two[1])
+    else:
+        assert max_abs(two[0], ref) < 2e-2 and max_abs(two[1], ref_lse) < LSE_TOL
+
+
+def test_in_launch_combine_on_two_streams(dev):
+    """Calls on two streams at once use separate arrival counters (one slab
+    per stream): interleaved, unsynchronised calls on both stay correct."""
+    q, k, v = _inputs(8, 24, 8, 4096, 128, torch.bfloat16, dev, seed=41)
+    q2, k2, v2 = _inputs(8, 24, 8, 4096, 128, torch.bfloat16, dev, seed=42)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    outs = []
+    for i in range(6):
+        st, (qq, kk, vv) = (s1, (q, k, v)) if i % 2 == 0 else (s2, (q2, k2, v2))
+        with torch.cuda.stream(st):
+            outs.append(_fd()(qq, kk, vv, num_splits=8))
+    torch.cuda.synchronize()
+    ref1, _ = ora.decode(q, k, v)
+    ref2, _ = ora.decode(q2, k2, v2)
+    for i, o in enumerate(outs):
+        assert max_abs(o, ref1 if i % 2 == 0 else ref2) < 2e-2, i
+
+
+def test_in_launch_combine_under_graph_replay(dev):
+    """A captured flash_decode (seq_lens, several splits) replayed at changing
+    lengths, with eager calls on the same stream between the replays, matches
+    the eager call every time."""
+    B, Hq, Hkv, T, D = 4, 24, 8, 4096, 128
+    q, k, v = _inputs(B, Hq, Hkv, T, D, torch.bfloat16, dev, seed=43)
+    sl = torch.full((B,), T, dtype=torch.int64, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _fd()(q, k, v, seq_lens=sl, num_splits=6)          # warm-up on the capture side
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g = _fd()(q, k, v, seq_lens=sl, num_splits=6)
+    for lens in ([4096, 1, 2000, 17], [33, 4095, 4096, 1024], [1, 1, 1, 1]):
+        sl.copy_(torch.tensor(lens, dtype=torch.int64))
+        graph.replay()
+        eager = _fd()(q, k, v, seq_lens=sl, num_splits=6)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, eager), lens
+        ref, _ = ora.decode(q, k, v, seq_lens=sl)
+        assert max_abs(out_g, ref) < 2e-2, lens

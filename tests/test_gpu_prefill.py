@@ -189,19 +189,21 @@ def test_fused_q_rope_fp32_and_mixed_tables(dev):
         _fa()(q, k, v, rope_cos=cos[:10], rope_sin=sin[:10])
 
 
-@pytest.mark.parametrize("D", [64, 128])
-def test_epilogue_store_paths_agree(dev, D):
-    """The kernels write 16-byte-aligned output rows through an LDS-staged
-    whole-row epilogue and other rows with 8-byte stores: an output buffer
-    offset by 8 bytes (rows 8- but not 16-byte aligned) takes the second
-    path and must hold the same bits."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("D", [32, 64, 128, 256])
+def test_epilogue_store_paths_agree(dev, D, dtype):
+    """The MFMA kernels (D 32 / 128 / 256 and the D 64 pipelined one) write
+    16-byte-aligned output rows through an LDS-staged whole-row epilogue and
+    other rows with 8-byte stores: an output buffer offset by 8 bytes (rows 8-
+    but not 16-byte aligned) takes the second path and must hold the same
+    bits."""
     from src import _lib
     B, Hq, Hkv, S = 2, 8, 2, 333
-    q = randn((B, Hq, S, D), 11, torch.bfloat16, dev)
-    k = randn((B, Hkv, S, D), 12, torch.bfloat16, dev)
-    v = randn((B, Hkv, S, D), 13, torch.bfloat16, dev)
+    q = randn((B, Hq, S, D), 11, dtype, dev)
+    k = randn((B, Hkv, S, D), 12, dtype, dev)
+    v = randn((B, Hkv, S, D), 13, dtype, dev)
     out, lse = _fa()(q, k, v, return_lse=True)
-    buf = torch.full((B * Hq * S * D + 8,), 5.0, device=dev, dtype=torch.bfloat16)
+    buf = torch.full((B * Hq * S * D + 8,), 5.0, device=dev, dtype=dtype)
     o = buf[4:4 + B * Hq * S * D].view(B, Hq, S, D)
     assert o.data_ptr() % 16 == 8
     lse2 = torch.empty_like(lse)

@@ -266,9 +266,15 @@ def test_quantized_attention_fuses_qkv_at_prefill_sizes(dev):
 def test_gemm_swiglu_is_the_unfused_chain(dev, M, K, N, dtype, sdtype):
     """silu(w1(x)) * w3(x) in one launch: the GEMM outputs are the unsplit
     single GEMM's bits, then silu and the product are rounded where separate
-    ops round; against that chain on the CPU (the kernel's silu uses the
-    hardware exp2 and reciprocal, so a few elements may be an ulp off) and the
-    fp32 oracle."""
+    ops round.  The kernel's silu (hardware exp2 and reciprocal) rounds to
+    the correctly rounded silu (float64, then the dtype) or to one of its two
+    neighbours: every output equals bf16(s * y3) for one of those three s
+    (an element-exact statement of "silu within one ulp"), and > 99 % of them
+    equal the chain with the correctly rounded silu.  The exception is silu
+    below 2^-100 (y1 < about -65): the hardware exp2 and reciprocal flush
+    fp32 denormals, so there the output may be 0 where the float64 silu is a
+    tiny number -- checked as an absolute difference below 2^-80.  Also
+    against the fp32 oracle."""
     from src.quant_linear import w8a16_gemm_mfma, w8a16_gemm_swiglu
     q1, s1 = _quantised(N, K, dtype, dev, 70)
     q3, s3 = _quantised(N, K, dtype, dev, 71)
@@ -276,11 +282,21 @@ def test_gemm_swiglu_is_the_unfused_chain(dev, M, K, N, dtype, sdtype):
     x = _x(M, K, dtype, dev, 72)
     y = w8a16_gemm_swiglu(x, q1, s1, q3, s3)
     assert y.shape == (M, N) and y.dtype == dtype
-    y1 = w8a16_gemm_mfma(x, q1, s1, splits=1).cpu().float()
+    y1 = w8a16_gemm_mfma(x, q1, s1, splits=1).cpu()
     y3 = w8a16_gemm_mfma(x, q3, s3, splits=1).cpu().float()
-    chain = (torch.nn.functional.silu(y1).to(dtype).float() * y3).to(dtype)
+    y1d = y1.double()
+    s_cr = (y1d / (1.0 + torch.exp(-y1d))).to(dtype)           # correctly rounded silu
+    bits = s_cr.view(torch.int16)
     yc = y.cpu()
-    assert (yc == chain).float().mean() > 0.99
+    chain = (s_cr.float() * y3).to(dtype)
+    ok = yc == chain
+    for step in (-1, 1):                                        # the neighbouring values
+        nb = (bits + step).view(dtype)
+        ok |= yc == (nb.float() * y3).to(dtype)
+    tiny = s_cr.float().abs() < 2.0 ** -100
+    ok |= tiny & ((yc.float() - chain.float()).abs() <= 2.0 ** -80)
+    assert bool(ok.all()), int((~ok).sum())
+    assert (yc == chain)[~tiny].float().mean() > 0.99
     assert _rel(yc, chain) < 1e-2
     ref = torch.nn.functional.silu(oq.w8a16(x, q1, s1).float()) * oq.w8a16(x, q3, s3).float()
     assert _rel(yc, ref) < 3e-2

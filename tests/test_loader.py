@@ -7,6 +7,8 @@ table targets), so the remap is checked against an independent source.  The
 forward-pass equivalence with transformers and the W8A16 quantisation on the
 device are in tests/test_gpu_loader.py.
 """
+import math
+
 import pytest
 import torch
 
@@ -138,3 +140,33 @@ def test_should_quantize_key():
     for key in ("output.weight", "tok_embeddings.weight", "norm.weight", "layers.0.attention_norm.weight",
                 "layers.0.ffn_norm.weight", "model.layers.0.self_attn.q_proj.weight", "layers.attention.wq.weight"):
         assert not should_quantize_key(key), key
+
+
+def test_accuracy_metrics_closed_forms():
+    from src import quant_utils as q
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(3, 5, 40, generator=g)
+    assert abs(float(q.cosine_similarity(a, a)) - 1) < 1e-6
+    assert abs(float(q.cosine_similarity(a, -a)) + 1) < 1e-6
+    e0, e1 = torch.zeros(2, 8), torch.zeros(2, 8)
+    e0[:, 0] = 1
+    e1[:, 1] = 3
+    assert float(q.cosine_similarity(e0, e1)) == 0.0
+    assert q.logits_max_abs_error(a, a + 0.25) == pytest.approx(0.25)
+    assert q.logits_relative_error(torch.full((4,), 2.0), torch.full((4,), 3.0)) == pytest.approx(0.5)
+    assert q.top1_agreement(a, a) == 1.0
+    b = a.clone()
+    b[0, 0] = -a[0, 0]                     # row (0, 0)'s argmax moves to its argmin
+    assert q.top1_agreement(a, b) == pytest.approx(14 / 15)
+    # uniform logits over V classes: perplexity V; a perfect predictor: 1
+    V = 37
+    labels = torch.randint(0, V, (2, 9), generator=g)
+    assert q.perplexity(torch.zeros(2, 9, V), labels) == pytest.approx(V, rel=1e-5)
+    sharp = torch.full((9, V), -1e4)
+    sharp[torch.arange(8), labels[0, 1:]] = 0.0
+    assert q.perplexity(sharp, labels[0]) == pytest.approx(1.0, abs=1e-5)
+    ign = labels.clone()
+    ign[:, 5:] = -100
+    lp = torch.log_softmax(torch.randn(2, 9, V, generator=g), -1)
+    ref = math.exp(-float(torch.stack([lp[b, t, ign[b, t + 1]] for b in range(2) for t in range(4)]).mean()))
+    assert q.perplexity(lp, ign) == pytest.approx(ref, rel=1e-5)

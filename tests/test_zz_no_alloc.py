@@ -69,3 +69,36 @@ def test_noalloc_rejects_partials_beyond_the_scratch(dev):
     assert st == -2
     from src import _lib
     assert "scratch" in _lib.load().mi_last_error().decode()
+
+
+def test_noalloc_under_graph_capture(dev):
+    """The stated use: two calls captured in one graph (the entry point
+    allocates nothing; the two calls share the library's array one after the
+    other),
+    replayed three times at changing lengths with eager work on the stream in
+    between; every replay matches flash_decode with a caller workspace bit
+    for bit."""
+    from src.flash_decode import flash_decode
+    print("noalloc graph: B8 Hq24 Hkv8 L2048 D128 splits 4 + B2 Hq8 Hkv2 L500 D64 splits 3",
+          flush=True)
+    qa, ka, va = (randn((8, 24, 1, 128), 50, device=dev), randn((8, 8, 2048, 128), 51, device=dev),
+                  randn((8, 8, 2048, 128), 52, device=dev))
+    qb, kb, vb = (randn((2, 8, 1, 64), 53, device=dev), randn((2, 2, 500, 64), 54, device=dev),
+                  randn((2, 2, 500, 64), 55, device=dev))
+    sla = torch.full((8,), 2048, dtype=torch.int64, device=dev)
+    slb = torch.full((2,), 500, dtype=torch.int64, device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        st_a, out_a, lse_a = _noalloc(qa, ka, va, seq_lens=sla, num_splits=4)
+        st_b, out_b, lse_b = _noalloc(qb, kb, vb, seq_lens=slb, num_splits=3)
+    assert st_a == 0 and st_b == 0
+    for la, lb in (([2048, 1, 700, 2047, 5, 1024, 1500, 3], [500, 17]),
+                   ([1] * 8, [1, 499]), ([999] * 8, [250, 250])):
+        sla.copy_(torch.tensor(la))
+        slb.copy_(torch.tensor(lb))
+        graph.replay()
+        ra, rla = flash_decode(qa, ka, va, seq_lens=sla, num_splits=4, return_lse=True)
+        rb, rlb = flash_decode(qb, kb, vb, seq_lens=slb, num_splits=3, return_lse=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out_a, ra) and torch.equal(lse_a, rla), la
+        assert torch.equal(out_b, rb) and torch.equal(lse_b, rlb), lb
