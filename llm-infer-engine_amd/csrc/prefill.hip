@@ -27,7 +27,9 @@
 //    src/flash_attn.py:63,72).
 //  * head_dim 64: a software-pipelined kernel (each wave overlaps its own
 //    MFMAs with its softmax, 4-slot LDS ring, one barrier per tile);
-//    head_dim 32 / 128: double-buffered tiles, one barrier per tile.
+//    head_dim 128: the same schedule with separate K and V double buffers and
+//    bank-conflict-free V reads; head_dim 32 / 256: double-buffered tiles,
+//    one barrier per tile.
 //  * The prologue issues the first tile copies before the Q loads (one memory
 //    round trip for both); the epilogue stages the output rows in the freed
 //    LDS and writes whole 2*D-byte rows with 16-byte lanes.
@@ -971,6 +973,508 @@ __global__ __launch_bounds__(256, 2) void prefill_sp_kernel(PrefillArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Software-pipelined kernel with separate K and V double buffers, head dims 64
+// and 128 (16-bit).  The slot schedule is prefill_sp_kernel's:
+//
+//   slot A(t): softmax(t.h0) | PV(t-1.h1), QK(t.h1)
+//   ---- wait for K(t+1) and V(t), barrier, copy K(t+2) and V(t+1) ----
+//   slot B(t): softmax(t.h1) | PV(t.h0),   QK(t+1.h0)
+//
+// K(t) is read in B(t-1) and A(t), V(t) in B(t) and A(t+1), so two slots of
+// each suffice: the copy into a slot starts at the barrier right after the
+// slot's previous tile was last read and has one slot pair to complete.  Four
+// tiles of LDS (64 KB at D = 128, where a 4-slot ring of K+V tiles would need
+// 128 KB), so two 4-wave blocks still share a CU.
+// A wave owns RB 32-row blocks: RB = 2 at D = 64 (every K/V operand feeds two
+// MFMAs), RB = 1 at D = 128 (the 32 x 128 fp32 O tile, Q and the operands of
+// a slot take the registers two waves per SIMD leave).  Head dim 128 runs this
+// kernel (119 us against 124 us for prefill_kernel<128> at B4 S2048 24/8
+// heads); head dim 64 keeps prefill_sp_kernel (77 us against 79 us here).  Row block rb starts
+// at row r0 + 32 rb; its phase is the half of a 64-key tile that row lies in.
+// On the wave's diagonal tile a phase-0 row block sees half 0 through the
+// causal triangle and none of half 1; a phase-1 row block sees half 0 whole
+// and half 1 through the triangle.  Row-block sets are bit masks (PART: row
+// blocks that take part, MSK: row blocks masked by the triangle).
+// V tile swizzle of the pipelined kernel (XOR of the 16-byte chunk index of
+// row r).  A half-wave's transposed V^T read touches rows r0..r0+3 (r0 a
+// multiple of 4) at byte offsets 0..63: at D = 128 (256-byte rows, one bank
+// row each) chunks ^ 4 (r & 3) put the four rows in the four quarters of the
+// banks, at D = 64 (two rows per bank row) chunks ^ 4 ((r >> 1) & 1) put rows
+// r0 + 2, r0 + 3 in the other halves of those of r0, r0 + 1 -- conflict-free
+// instead of 4-way / 2-way.  Only chunk bits 2-3 change, and rows 16 apart
+// share the swizzle.
+template <int D>
+__device__ inline int v_swz2(int r) { return D == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); }
+
+template <typename T, int D>
+__global__ __launch_bounds__(256, 2) void prefill_sp2_kernel(PrefillArgs a) {
+  using MM = Mfma<T>;
+  typedef typename MM::v8 v8;
+  constexpr int RB = D == 64 ? 2 : 1;
+  constexpr int BN = 64, KCH = D / 8, DC = D / 16, DB = D / 32;
+  constexpr int ROW_B = D * 2, TILE_B = BN * ROW_B;
+  constexpr int NI = TILE_B / 1024 / 4;        // 1 KB copies per wave per K (V) tile
+  static_assert(NI * 4 * 1024 == TILE_B, "tile must split into 1 KB wave copies");
+  constexpr int ALL = (1 << RB) - 1;
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  unsigned char* const lds = smem_raw;         // K slot 0 | K slot 1 | V slot 0 | V slot 1
+
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int hh = lane >> 5, lr = lane & 31;
+
+  // ---- block -> (batch, kv head, head chunk, position block), heavy first,
+  //      all blocks of one (b, kvh, chunk) on one XCD
+  const int n_pairs = a.B * a.Hkv * a.head_chunks;
+  const int bid = blockIdx.x;
+  int pair, pb_rank;
+  if ((n_pairs & 7) == 0) {
+    const int xcd = bid & 7, slot = bid >> 3, ppx = n_pairs >> 3;
+    pair = xcd * ppx + slot % ppx;
+    pb_rank = slot / ppx;
+  } else {
+    pair = bid % n_pairs;
+    pb_rank = bid / n_pairs;
+  }
+  const int pb = a.n_pb - 1 - pb_rank;
+  const int hc = pair % a.head_chunks;
+  const int kvh = (pair / a.head_chunks) % a.Hkv;
+  const int b = pair / (a.head_chunks * a.Hkv);
+  const int GH = a.heads_per_block, PJ = a.pj;
+  constexpr int RW = 32 * RB;                         // query rows per wave
+  const int p0 = pb * RW * PJ;
+  const int g = w % GH, j = w / GH;
+  const int head = kvh * a.G + hc * GH + g;
+  const int r0 = p0 + RW * j;                         // first query row of this wave
+  const int ph0 = (r0 >> 5) & 1;                      // phase of row block 0 (0 at RB = 2)
+  const int n_tw = r0 < a.S ? r0 / BN + 1 : 0;        // tiles this wave reads (last = diagonal)
+  const int n_tiles = (min(p0 + RW * PJ, a.S) - 1) / BN + 1;  // tiles the block copies
+
+  v8 qreg[RB][DC];
+
+  // ---- tile copies: wave w copies 1 KB pieces (w*NI + i) of each tile
+  const unsigned char* kbase = reinterpret_cast<const unsigned char*>(a.k) +
+                               ((int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh) * 2;
+  const unsigned char* vbase = reinterpret_cast<const unsigned char*>(a.v) +
+                               ((int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh) * 2;
+  const uint32_t lds_k = lds_addr(lds) + w * NI * 1024, lds_v = lds_k + 2 * TILE_B;
+  // copy the K (IS_V false) or V tile t into its slot t % 2; the lane -> chunk
+  // geometry is recomputed per tile rather than kept in registers
+  auto issue = [&](int t, auto is_v_c) __attribute__((always_inline)) {
+    constexpr bool IS_V = decltype(is_v_c)::value;
+    const int r0t = t * BN;
+    const int64_t ss = IS_V ? a.v_ss : a.k_ss;
+    const unsigned char* tb = (IS_V ? vbase : kbase) + (int64_t)r0t * ss * 2;
+    const uint32_t dst = (IS_V ? lds_v : lds_k) + (t & 1) * TILE_B;
+    const int lim = a.S - 1 - r0t;   // rows past S are clamped (masked out later)
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int idx = (w * NI + i) * 64 + lane;   // physical chunk index in the tile
+      const int r = idx / KCH, pc = idx % KCH;
+      const int rr = min(r, lim);
+      const int lc = pc ^ (IS_V ? v_swz2<D>(r) : k_swz<D>(r));
+      lds_dma16(tb, (uint32_t)(rr * ss + lc * 8) * 2u, dst + i * 1024);
+    }
+  };
+  auto kslot = [&](int t) __attribute__((always_inline)) { return lds + (t & 1) * TILE_B; };
+  auto vslot = [&](int t) __attribute__((always_inline)) { return lds + (2 + (t & 1)) * TILE_B; };
+
+  // ---- per-lane operand read offsets (bytes, within one slot)
+  const int prow = perm_row(lr);
+  int k_rd[DC];
+#pragma unroll
+  for (int c = 0; c < DC; ++c) k_rd[c] = prow * ROW_B + (((2 * c + hh) ^ k_swz<D>(prow)) * 16);
+  // V^T operand rows r = 32*half + 16*cc + 8*(gq>>1) + 4*part + (sl>>2), dims
+  // 32 db + d0 .. +3: the swizzle changes the chunk's bits 2-3 (which db
+  // selects) by a value of `part` and the lane, so one base offset per
+  // (part, db) plus immediates address every read.
+  const int gq = lane >> 4, sl = lane & 15;
+  int v_rd[2][DB];
+#pragma unroll
+  for (int part = 0; part < 2; ++part) {
+    const int r = 8 * (gq >> 1) + 4 * part + (sl >> 2);
+    const int d0 = 16 * (gq & 1) + 4 * (sl & 3);
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+      v_rd[part][db] = r * ROW_B + (((d0 >> 3) + 4 * db) ^ v_swz2<D>(r)) * 16 + (d0 & 7) * 2;
+  }
+  // causal triangle of a diagonal half: score i of this lane is key offset
+  // kk(i) within the half, visible iff kk(i) <= tri
+  const int tri = lr - 8 * hh;
+
+  f32x16 o[RB][DB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[rb][db][i] = 0.f;
+  float m[RB], l[RB], alpha[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) { m[rb] = kNegBig; l[rb] = 0.f; alpha[rb] = 1.f; }
+  const float sl2 = a.scale_log2;
+  f32x16 sA[RB], sB[RB];   // scores of the current / next half
+  v8 pA[RB][2], pB[RB][2]; // P^T of half 0 / half 1 of a tile
+
+  // S^T for one half (K rows 32h..32h+31 of the tile in K slot ks)
+  auto qk = [&](const unsigned char* ks, int h, f32x16 (&s)[RB], auto part_c) __attribute__((always_inline)) {
+    constexpr int PART = decltype(part_c)::value;
+    if constexpr (PART != 0) {
+      v8 ka[DC];
+#pragma unroll
+      for (int c = 0; c < DC; ++c)
+        ka[c] = __builtin_bit_cast(v8, *reinterpret_cast<const u32x4*>(ks + k_rd[c] + h * 32 * ROW_B));
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb)
+        if ((PART >> rb) & 1)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[rb][i] = 0.f;
+#pragma unroll
+      for (int c = 0; c < DC; ++c)
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+          if ((PART >> rb) & 1) s[rb] = MM::mma(ka[c], qreg[rb][c], s[rb]);
+    }
+  };
+  // O^T += V^T P^T for one half (V rows 32h..32h+31 of the tile in V slot vs)
+  auto pv = [&](const unsigned char* vs, int h, const v8 (&p)[RB][2], auto part_c) __attribute__((always_inline)) {
+    constexpr int PART = decltype(part_c)::value;
+    if constexpr (PART != 0) {
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+        for (int db = 0; db < DB; ++db) {
+          const int off = (32 * h + 16 * cc) * ROW_B;
+          const uint2 lo = lds_read_tr(vs + v_rd[0][db] + off);
+          const uint2 hi = lds_read_tr(vs + v_rd[1][db] + off);
+          const v8 vv = __builtin_bit_cast(v8, u32x4{lo.x, lo.y, hi.x, hi.y});
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb)
+            if ((PART >> rb) & 1) o[rb][db] = MM::mma(vv, p[rb][cc], o[rb][db]);
+        }
+    }
+  };
+  // PV of one half (V slot vs, half hv) and QK of another (K slot ks, half hk)
+  // for every row block, as DC steps of one K operand read, one V^T operand
+  // read and their MFMAs, so that each step's LDS reads are in flight while
+  // the previous step's MFMAs run (the two products are independent; reads and
+  // MFMAs issued as separate loops end up as read, wait, MFMA at these
+  // register counts).
+  auto pvqk = [&](const unsigned char* vs, int hv, const v8 (&p)[RB][2],
+                  const unsigned char* ks, int hk, f32x16 (&s)[RB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s[rb][i] = 0.f;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      const int cc = c / DB, db = c % DB;    // PV step c: 16 keys cc, 32 dims db
+      const v8 ka = __builtin_bit_cast(v8, *reinterpret_cast<const u32x4*>(ks + k_rd[c] + hk * 32 * ROW_B));
+      const int off = (32 * hv + 16 * cc) * ROW_B;
+      const uint2 lo = lds_read_tr(vs + v_rd[0][db] + off);
+      const uint2 hi = lds_read_tr(vs + v_rd[1][db] + off);
+      const v8 vv = __builtin_bit_cast(v8, u32x4{lo.x, lo.y, hi.x, hi.y});
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) s[rb] = MM::mma(ka, qreg[rb][c], s[rb]);
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) o[rb][db] = MM::mma(vv, p[rb][cc], o[rb][db]);
+    }
+  };
+  // Online softmax of one half for the row blocks of PART (MSK: with the
+  // causal triangle).  The running max and sum are updated without branches
+  // (alpha = 1 when the max stays); the returned flag says whether O must be
+  // rescaled once the half's MFMAs are done.
+  auto smax = [&](f32x16 (&s)[RB], v8 (&p)[RB][2], auto part_c, auto msk_c) __attribute__((always_inline)) {
+    constexpr int PART = decltype(part_c)::value, MSK = decltype(msk_c)::value;
+    float mx[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      mx[rb] = kNegBig;
+      if (!((PART >> rb) & 1)) continue;
+      if ((MSK >> rb) & 1) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (16 * (i >> 3) + (i & 7) > tri) s[rb][i] = -INFINITY;
+      }
+      float x = fmaxf(fmaxf(s[rb][0], s[rb][1]), s[rb][2]);
+#pragma unroll
+      for (int i = 3; i < 15; i += 2) x = fmaxf(fmaxf(x, s[rb][i]), s[rb][i + 1]);
+      x = fmaxf(x, s[rb][15]);
+      auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+      mx[rb] = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl2;
+    }
+    bool up = false;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      if ((PART >> rb) & 1) up = up || mx[rb] > m[rb] + kRescaleThreshold;
+    const bool resc = __builtin_amdgcn_ballot_w64(up) != 0;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      if (!((PART >> rb) & 1)) continue;
+      const float m_new = resc ? fmaxf(m[rb], mx[rb]) : m[rb];
+      alpha[rb] = fast_exp2(m[rb] - m_new);
+      m[rb] = m_new;
+      const float mr = m_new;
+      float ls0 = 0.f, ls1 = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        uint32_t wd[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float e0 = fast_exp2(fmaf(s[rb][8 * cc + 2 * t], sl2, -mr));
+          const float e1 = fast_exp2(fmaf(s[rb][8 * cc + 2 * t + 1], sl2, -mr));
+          if (t & 1) ls1 += e0 + e1; else ls0 += e0 + e1;
+          wd[t] = MM::pack2(e0, e1);
+        }
+        p[rb][cc] = __builtin_bit_cast(v8, u32x4{wd[0], wd[1], wd[2], wd[3]});
+      }
+      l[rb] = fmaf(l[rb], alpha[rb], ls0 + ls1);
+      // keep this half's softmax inside its slot: without a use here the
+      // compiler sinks it past the tile barrier into the next slot
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+        __asm__ volatile("" ::"v"(__builtin_bit_cast(u32x4, p[rb][cc])));
+      __asm__ volatile("" ::"v"(l[rb]), "v"(m[rb]));
+    }
+    return resc;
+  };
+  // Softmax of one half against the running max, without the half's own max
+  // (prefill_sp_kernel's smax_fast): while a lane's row sum of the half stays
+  // at or below 16 * 2^kRescaleThreshold no p exceeds 2^(kRescaleThreshold+4)
+  // and the running max may stay.  Returns true (uniform over the wave) when
+  // some lane's sum is larger; the caller then runs smax on the same scores.
+  auto smax_fast = [&](f32x16 (&s)[RB], v8 (&p)[RB][2], auto part_c, auto msk_c) __attribute__((always_inline)) {
+    constexpr int PART = decltype(part_c)::value, MSK = decltype(msk_c)::value;
+    float lsum[RB];
+    bool big = false;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      lsum[rb] = 0.f;
+      if (!((PART >> rb) & 1)) continue;
+      if ((MSK >> rb) & 1) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (16 * (i >> 3) + (i & 7) > tri) s[rb][i] = -INFINITY;
+      }
+      const float mr = m[rb];
+      float ls0 = 0.f, ls1 = 0.f;
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        uint32_t wd[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float e0 = fast_exp2(fmaf(s[rb][8 * cc + 2 * t], sl2, -mr));
+          const float e1 = fast_exp2(fmaf(s[rb][8 * cc + 2 * t + 1], sl2, -mr));
+          if (t & 1) ls1 += e0 + e1; else ls0 += e0 + e1;
+          wd[t] = MM::pack2(e0, e1);
+        }
+        p[rb][cc] = __builtin_bit_cast(v8, u32x4{wd[0], wd[1], wd[2], wd[3]});
+      }
+      lsum[rb] = ls0 + ls1;
+      big = big || !(lsum[rb] <= kFastSumLimit);
+    }
+    const bool fb = __builtin_amdgcn_ballot_w64(big) != 0;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      if (!((PART >> rb) & 1)) continue;
+      l[rb] = fb ? l[rb] : l[rb] + lsum[rb];
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+        __asm__ volatile("" ::"v"(__builtin_bit_cast(u32x4, p[rb][cc])));
+      __asm__ volatile("" ::"v"(l[rb]));
+    }
+    return fb;
+  };
+  auto rescale_o = [&](auto part_c) __attribute__((always_inline)) {
+    constexpr int PART = decltype(part_c)::value;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      if (!((PART >> rb) & 1)) continue;
+#pragma unroll
+      for (int db = 0; db < DB; ++db)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[rb][db][i] *= alpha[rb];
+    }
+  };
+  // Issue order of a steady-state slot: the slot's LDS operand reads first,
+  // then one MFMA followed by a run of softmax VALU work, repeated (a wave's
+  // own VALU issue stalls for about half of each 32x32x16 MFMA).
+  // Steady-state slot order: pvqk's step c + 1 reads (one K, two V^T) are
+  // issued before step c's MFMAs, and a run of softmax VALU work follows each
+  // MFMA (a wave's own VALU issue stalls for about half of each 32x32x16
+  // MFMA, so the softmax spreads over the matrix work).
+  constexpr int kVa0 = D == 64 ? 12 : 6, kVa = D == 64 ? 7 : 4;
+  auto interleave = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);     // step 0 reads
+    __builtin_amdgcn_sched_group_barrier(0x402, kVa0, 0);  // VALU (incl. exp)
+#pragma unroll
+    for (int c = 0; c < DC; ++c) {
+      if (c + 1 < DC) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);   // step c+1 reads
+#pragma unroll
+      for (int m = 0; m < 2 * RB; ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x402, kVa, 0);  // VALU
+      }
+    }
+  };
+  using TT = std::true_type;
+  using FF = std::false_type;
+  using IAll = std::integral_constant<int, ALL>;
+  using I0 = std::integral_constant<int, 0>;
+  // slot A(t): softmax(t.h0) | PV(t-1.h1), QK(t.h1).  HAS_PV: t > 0 (tile t-1
+  // is below the diagonal: every row block takes part in PV(t-1.h1)).  P_H1:
+  // row blocks that see half 1 of tile t; M_H0: row blocks whose half 0 is
+  // the causal triangle (both ALL / 0 below the diagonal).
+  auto slot_a = [&](int t, auto has_pv_c, auto p_h1_c, auto m_h0_c) __attribute__((always_inline)) {
+    constexpr bool HAS_PV = decltype(has_pv_c)::value;
+    constexpr int P_H1 = decltype(p_h1_c)::value, M_H0 = decltype(m_h0_c)::value;
+    if constexpr (HAS_PV && P_H1 == ALL) {
+      pvqk(vslot(t - 1), 1, pB, kslot(t), 1, sB);
+    } else {
+      if constexpr (HAS_PV) pv(vslot(t - 1), 1, pB, IAll{});
+      qk(kslot(t), 1, sB, p_h1_c);
+    }
+    if constexpr (!HAS_PV) {  // the wave's first tile: no running max yet, O still zero
+      smax(sA, pA, IAll{}, m_h0_c);
+    } else {
+      const bool fb = smax_fast(sA, pA, IAll{}, m_h0_c);
+      if constexpr (P_H1 == ALL && M_H0 == 0) interleave();
+      if (fb) {
+        if (smax(sA, pA, IAll{}, m_h0_c)) rescale_o(IAll{});
+      }
+    }
+  };
+  // slot B(t): softmax(t.h1) | PV(t.h0), QK(t+1.h0); on the diagonal tile the
+  // softmax of half 1 for the row blocks P_H1 that see it, then their drain
+  // PV(t.h1).
+  auto slot_b = [&](int t, auto diag_c, auto p_h1_c) __attribute__((always_inline)) {
+    constexpr bool DIAG = decltype(diag_c)::value;
+    constexpr int P_H1 = decltype(p_h1_c)::value;
+    if constexpr (!DIAG) {
+      pvqk(vslot(t), 0, pA, kslot(t + 1), 0, sA);
+      const bool fb = smax_fast(sB, pB, IAll{}, I0{});
+      interleave();
+      if (fb) {
+        if (smax(sB, pB, IAll{}, I0{})) rescale_o(IAll{});
+      }
+    } else if constexpr (P_H1 == 0) {
+      pv(vslot(t), 0, pA, IAll{});
+    } else {
+      pv(vslot(t), 0, pA, IAll{});
+      if (smax_fast(sB, pB, p_h1_c, p_h1_c)) {
+        if (smax(sB, pB, p_h1_c, p_h1_c)) rescale_o(p_h1_c);
+      }
+      pv(vslot(t), 1, pB, p_h1_c);
+    }
+  };
+  // the diagonal tile's slots: at RB = 2 row block 0 is phase 0 and row block 1
+  // phase 1; at RB = 1 the wave's one row block has phase PH (the phase of its
+  // first row, a compile-time branch of the whole tile loop below: a branch on
+  // it inside the loop leaves the register allocator 100+ spills)
+  auto diag_a = [&](int t, auto has_pv_c, auto ph_c) __attribute__((always_inline)) {
+    constexpr int PH = decltype(ph_c)::value;
+    if constexpr (RB == 2)
+      slot_a(t, has_pv_c, std::integral_constant<int, 2>{}, std::integral_constant<int, 1>{});
+    else if constexpr (PH == 0)
+      slot_a(t, has_pv_c, I0{}, std::integral_constant<int, 1>{});
+    else
+      slot_a(t, has_pv_c, std::integral_constant<int, 1>{}, I0{});
+  };
+  auto diag_b = [&](int t, auto ph_c) __attribute__((always_inline)) {
+    constexpr int PH = decltype(ph_c)::value;
+    if constexpr (RB == 2)
+      slot_b(t, TT{}, std::integral_constant<int, 2>{});
+    else if constexpr (PH == 0)
+      slot_b(t, TT{}, I0{});
+    else
+      slot_b(t, TT{}, std::integral_constant<int, 1>{});
+  };
+  // wait for K(t+1) and V(t), publish them, then copy K(t+2) into the slot
+  // K(t) (last read in slot A(t)) released and V(t+1) into V(t-1)'s
+  auto sync_tile = [&](int t) __attribute__((always_inline)) {
+    dma_wait_all();
+    block_sync_lds();
+    if (t + 2 < n_tiles) issue(t + 2, FF{});
+    if (t + 1 < n_tiles) issue(t + 1, TT{});
+  };
+
+  // ---- prologue: K(0), V(0), K(1) in flight, then Q (and its RoPE table
+  //      rows), so the copies and the Q loads share one memory round trip.
+  //      Rows past S read row S - 1: finite scores in rows whose output is
+  //      never stored.
+  issue(0, FF{});
+  issue(0, TT{});
+  if (n_tiles > 1) issue(1, FF{});
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int qrow = min(r0 + 32 * rb + lr, a.S - 1);
+    const T* qp = reinterpret_cast<const T*>(a.q) + (int64_t)b * a.q_sb +
+                  (int64_t)head * a.q_sh + (int64_t)qrow * a.q_ss;
+#pragma unroll
+    for (int c = 0; c < DC; ++c) qreg[rb][c] = __builtin_bit_cast(v8, load16(qp + 16 * c + 8 * hh));
+    if (a.rcos != nullptr) rope_q_fragments<T, DC>(a, qrow, hh, qreg[rb]);
+  }
+  dma_wait_all();
+  block_sync_lds();
+  auto run = [&](auto ph_c) __attribute__((always_inline)) {
+    int t = 0;
+    if (n_tw > 0) {
+      qk(kslot(0), 0, sA, IAll{});
+      if (n_tw == 1) {
+        diag_a(0, FF{}, ph_c);
+        sync_tile(0);
+        diag_b(0, ph_c);
+      } else {
+        slot_a(0, FF{}, IAll{}, I0{});
+        sync_tile(0);
+        slot_b(0, FF{}, IAll{});
+        for (t = 1; t < n_tw - 1; ++t) {   // steady state
+          slot_a(t, TT{}, IAll{}, I0{});
+          sync_tile(t);
+          slot_b(t, FF{}, IAll{});
+        }
+        diag_a(t, TT{}, ph_c);             // diagonal tile
+        sync_tile(t);
+        diag_b(t, ph_c);
+      }
+      t = n_tw;
+    }
+    for (; t < n_tiles; ++t) sync_tile(t);   // the block's remaining tiles
+  };
+  if (RB == 2 || ph0 == 0)
+    run(I0{});
+  else
+    run(std::integral_constant<int, 1>{});
+
+  if (n_tw == 0) return;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    float lt = l[rb];
+    {  // both lane halves hold partial sums of the same row
+      auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(lt), __float_as_uint(lt), false, false);
+      lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    const int qrow = r0 + 32 * rb + lr;
+    if (qrow >= a.S) continue;
+    const float inv = 1.0f / lt;
+    T* op = reinterpret_cast<T*>(a.o) + (int64_t)b * a.o_sb + (int64_t)head * a.o_sh +
+            (int64_t)qrow * a.o_ss;
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = 32 * db + 8 * q4 + 4 * hh;
+        const uint32_t w0 = MM::pack2(o[rb][db][4 * q4] * inv, o[rb][db][4 * q4 + 1] * inv);
+        const uint32_t w1 = MM::pack2(o[rb][db][4 * q4 + 2] * inv, o[rb][db][4 * q4 + 3] * inv);
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u32x2*>(op + d) = u32x2{w0, w1};
+      }
+    if (a.lse != nullptr && hh == 0)
+      a.lse[((int64_t)b * a.Hq + head) * a.S + qrow] = (m[rb] + __log2f(lt)) * kLn2;
+  }
+}
+
 // Plain VALU flash attention in fp32 arithmetic: every head dim of fp32
 // inputs (no fp32 MFMA tiles), and head dims 16 and 256 of bf16/fp16 inputs
 // (the MFMA kernels cover 32, 64 and 128).  TPR = D/8 lanes per query row, 8
@@ -1128,6 +1632,15 @@ hipError_t launch_valu(const PrefillArgs& a, int64_t head_dim, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <typename T, int D>
+hipError_t launch_sp2(const PrefillArgs& a, hipStream_t stream) {
+  const int n_pairs = a.B * a.Hkv * a.head_chunks;
+  dim3 grid((unsigned)(n_pairs * a.n_pb));
+  constexpr size_t smem = 4 * 64 * D * sizeof(T);  // K and V tiles, two slots each
+  hipLaunchKernelGGL((prefill_sp2_kernel<T, D>), grid, dim3(256), smem, stream, a);
+  return hipGetLastError();
+}
+
 template <typename T>
 hipError_t launch_sp(const PrefillArgs& a, hipStream_t stream) {
   const int n_pairs = a.B * a.Hkv * a.head_chunks;
@@ -1245,11 +1758,11 @@ int32_t attn_prefill(const void* q, const void* k, const void* v, void* o, float
   } else if (dtype == MI_DTYPE_BF16) {
     e = sp ? launch_sp<bf16_t>(a, st)
         : head_dim == 32 ? launch<bf16_t, 32>(a, nwaves, st)
-        : head_dim == 128 ? launch<bf16_t, 128>(a, nwaves, st) : launch<bf16_t, 256>(a, nwaves, st);
+        : head_dim == 128 ? launch_sp2<bf16_t, 128>(a, st) : launch<bf16_t, 256>(a, nwaves, st);
   } else {
     e = sp ? launch_sp<f16_t>(a, st)
         : head_dim == 32 ? launch<f16_t, 32>(a, nwaves, st)
-        : head_dim == 128 ? launch<f16_t, 128>(a, nwaves, st) : launch<f16_t, 256>(a, nwaves, st);
+        : head_dim == 128 ? launch_sp2<f16_t, 128>(a, st) : launch<f16_t, 256>(a, nwaves, st);
   }
   if (e != hipSuccess) {
     set_last_error("attn_prefill: launch failed: %s", hipGetErrorString(e));
