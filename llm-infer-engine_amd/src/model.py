@@ -122,10 +122,15 @@ class Attention(nn.Module):
 
 
 class TransformerBlock(nn.Module):
+    #: the block's attention and feed-forward classes (a subclass swaps in
+    #: variants with fused kernels; the parameter names stay the same)
+    attention_cls = Attention
+    feed_forward_cls = FeedForward
+
     def __init__(self, args, linear=nn.Linear):
         super().__init__()
-        self.attention = Attention(args, linear)
-        self.feed_forward = FeedForward(args.dim, args.hidden_dim, linear)
+        self.attention = self.attention_cls(args, linear)
+        self.feed_forward = self.feed_forward_cls(args.dim, args.hidden_dim, linear)
         self.attention_norm = RMSNorm(args.dim, eps=args.norm_eps)
         self.ffn_norm = RMSNorm(args.dim, eps=args.norm_eps)
 

@@ -27,8 +27,8 @@ from .quant_utils import quantize_weight_symmetric_per_channel
 
 
 class QuantizedFeedForward(FeedForward):
-    def __init__(self, dim: int, hidden_dim: int):
-        super().__init__(dim, hidden_dim, W8A16Linear)
+    def __init__(self, dim: int, hidden_dim: int, linear=W8A16Linear):
+        super().__init__(dim, hidden_dim, linear)
 
     def forward(self, x, *, residual=None):
         """Prefill-sized inputs: silu(w1(x)) * w3(x) in one GEMM launch (the
@@ -61,8 +61,8 @@ def _project_residual(lin, h, residual):
 
 
 class QuantizedAttention(Attention):
-    def __init__(self, args):
-        super().__init__(args, W8A16Linear)
+    def __init__(self, args, linear=W8A16Linear):
+        super().__init__(args, linear)
 
     def out_proj(self, output, residual=None):
         return _project_residual(self.wo, output, residual)
@@ -83,6 +83,10 @@ class QuantizedAttention(Attention):
 class QuantizedTransformerBlock(TransformerBlock):
     #: run single-token decode through the fused decode-layer kernels
     fused_decode = True
+    #: prefill-sized inputs: q|k|v in one GEMM launch, wo / w2 with the
+    #: residual add in their epilogues, silu(w1) * w3 in one launch
+    attention_cls = QuantizedAttention
+    feed_forward_cls = QuantizedFeedForward
 
     def __init__(self, args, linear=W8A16Linear):
         super().__init__(args, W8A16Linear)

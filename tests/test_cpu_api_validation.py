@@ -105,3 +105,24 @@ def test_rope_and_cache_update_rejects_shapes_the_cache_does_not_hold(shape, lay
     cos = torch.ones(1, shape[3] // 2, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match=msg):
         rope_and_cache_update(_t(*shape), _t(*shape), cos, cos, kv, layer, start_pos=0)
+
+
+def test_quantized_blocks_run_the_fused_prefill_classes():
+    """Llama3Quantized's blocks hold QuantizedAttention / QuantizedFeedForward
+    (one-launch q|k|v, SwiGLU and residual epilogues at prefill sizes), with
+    the parameter names of the plain modules (the checkpoint format), and the
+    plain Llama3 keeps the plain ones."""
+    import torch
+    from src.config import ModelArgs
+    from src.model import Attention, FeedForward, Llama3
+    from src.model_quantized import Llama3Quantized, QuantizedAttention, QuantizedFeedForward
+    args = ModelArgs(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, vocab_size=64, hidden_dim=512)
+    with torch.device("meta"):
+        mq, mp = Llama3Quantized(args), Llama3(args)
+    for layer in mq.layers:
+        assert isinstance(layer.attention, QuantizedAttention)
+        assert isinstance(layer.feed_forward, QuantizedFeedForward)
+    for layer in mp.layers:
+        assert type(layer.attention) is Attention and type(layer.feed_forward) is FeedForward
+    kq, kp = set(mq.state_dict()), set(mp.state_dict())
+    assert kp <= kq and all(k.endswith(".scales") for k in kq - kp)
