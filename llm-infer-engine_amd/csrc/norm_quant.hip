@@ -2,7 +2,7 @@
 //
 // RMSNorm (src/rms_norm.py:18-39): y = x * rsqrt(sum(x^2)/N + eps) * w, all in
 // fp32 from the stored values, rounded once to x's dtype.  One workgroup per
-// row; wave shuffles + LDS for the sum of squares.
+// row; wave shuffles + LDS for the sum of squares; 16-byte rows in registers.
 //
 // Quantiser (src/quant_utils.py:7-36): per output row n,
 //   amax = max(max_k |w[n,k]|, 1e-12)          (fp32)
@@ -47,6 +47,61 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(NormArgs a) {
   for (int i = tid; i < a.N; i += 256) {
     const float v = Elem<T>::to_f32(xr[i]);
     yr[i] = Elem<T>::from_f32(v * rstd * Elem<WT>::to_f32(w[i]));
+  }
+}
+
+// 2-byte rows of N <= 2048 * CPT elements with 16-byte aligned rows and
+// weights: each thread loads its 16-byte chunks of the row once, keeps them in
+// registers across the reduction and writes 16-byte chunks (one read and one
+// write of the row instead of two reads with 2-byte accesses).  The same fp32
+// maths as rmsnorm_kernel; the sum of squares is taken over a thread's 8
+// contiguous elements first (fp32 summation order only).
+template <typename T, typename WT, int CPT>
+__global__ __launch_bounds__(256) void rmsnorm_vec_kernel(NormArgs a) {
+  __shared__ float red[4];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const T* xr = reinterpret_cast<const T*>(a.x) + (int64_t)row * a.x_rs;
+  T* yr = reinterpret_cast<T*>(a.y) + (int64_t)row * a.y_rs;
+  const WT* w = reinterpret_cast<const WT*>(a.w);
+  const int nch = a.N >> 3;
+  u32x4 xv[CPT];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int idx = tid + c * 256;
+    if (idx < nch) {
+      xv[c] = load16(xr + 8 * idx);
+      float f[8];
+      Chunk<T>::unpack(xv[c], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) ss += shfl_xor_f32(ss, off);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  const float tot = red[0] + red[1] + red[2] + red[3];
+  const float rstd = 1.0f / sqrtf(tot / (float)a.N + a.eps);
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) {
+    const int idx = tid + c * 256;
+    if (idx < nch) {
+      float f[8], wf[8];
+      Chunk<T>::unpack(xv[c], f);
+      if constexpr (sizeof(WT) == 2) {
+        Chunk<WT>::unpack(load16(w + 8 * idx), wf);
+      } else {
+        const f32x4 w0 = *reinterpret_cast<const f32x4*>(w + 8 * idx);
+        const f32x4 w1 = *reinterpret_cast<const f32x4*>(w + 8 * idx + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { wf[e] = w0[e]; wf[4 + e] = w1[e]; }
+      }
+      union { u32x4 u; T t[8]; } o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o.t[e] = Elem<T>::from_f32(f[e] * rstd * wf[e]);
+      *reinterpret_cast<u32x4*>(yr + 8 * idx) = o.u;
+    }
   }
 }
 
@@ -105,13 +160,28 @@ extern "C" int32_t mi_rmsnorm(const void* x, const void* w, void* y,
   NormArgs a{x, w, y, x_rs, y_rs, (int32_t)rows, (int32_t)n, eps};
   dim3 grid((unsigned)rows), block(256);
   hipStream_t st = (hipStream_t)stream;
-#define MI_NORM(T, WT) hipLaunchKernelGGL((rmsnorm_kernel<T, WT>), grid, block, 0, st, a)
+  // 16-byte rows take the vector kernel (CPT chunks of 8 per thread)
+  const bool vec = dtype != MI_DTYPE_F32 && n % 8 == 0 && n <= 8192 &&
+                   ((uintptr_t)x | (uintptr_t)y | (uintptr_t)w) % 16 == 0 &&
+                   ((x_rs | y_rs) * 2) % 16 == 0;
+  const int cpt = (int)((n / 8 + 255) / 256);
+#define MI_NORM(T, WT)                                                                   \
+  if (!vec)                                                                              \
+    hipLaunchKernelGGL((rmsnorm_kernel<T, WT>), grid, block, 0, st, a);                 \
+  else if (cpt == 1)                                                                     \
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, WT, 1>), grid, block, 0, st, a);          \
+  else if (cpt == 2)                                                                     \
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, WT, 2>), grid, block, 0, st, a);          \
+  else                                                                                   \
+    hipLaunchKernelGGL((rmsnorm_vec_kernel<T, WT, 4>), grid, block, 0, st, a)
   if (dtype == MI_DTYPE_BF16 && wdtype == MI_DTYPE_BF16) MI_NORM(bf16_t, bf16_t);
   else if (dtype == MI_DTYPE_BF16 && wdtype == MI_DTYPE_F32) MI_NORM(bf16_t, float);
   else if (dtype == MI_DTYPE_F16 && wdtype == MI_DTYPE_F16) MI_NORM(f16_t, f16_t);
   else if (dtype == MI_DTYPE_F16 && wdtype == MI_DTYPE_F32) MI_NORM(f16_t, float);
-  else if (dtype == MI_DTYPE_F32 && wdtype == MI_DTYPE_F32) MI_NORM(float, float);
-  else if (dtype == MI_DTYPE_F32 && wdtype == MI_DTYPE_BF16) MI_NORM(float, bf16_t);
+  else if (dtype == MI_DTYPE_F32 && wdtype == MI_DTYPE_F32)
+    hipLaunchKernelGGL((rmsnorm_kernel<float, float>), grid, block, 0, st, a);
+  else if (dtype == MI_DTYPE_F32 && wdtype == MI_DTYPE_BF16)
+    hipLaunchKernelGGL((rmsnorm_kernel<float, bf16_t>), grid, block, 0, st, a);
   else {
     set_last_error("rmsnorm: unsupported dtype pair (%d, %d)", (int)dtype, (int)wdtype);
     return MI_ERR_UNSUPPORTED;

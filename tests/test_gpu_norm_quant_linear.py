@@ -106,6 +106,34 @@ def test_rmsnorm(dev, dtype):
     assert max_abs(y, ref) < tol * float(ref.float().abs().max())
 
 
+@pytest.mark.parametrize("N", [8, 1000, 2048, 2056, 4104, 8192, 8200, 100])
+@pytest.mark.parametrize("dtype,wdtype", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                          (torch.bfloat16, torch.float32)])
+def test_rmsnorm_row_widths(dev, N, dtype, wdtype):
+    """Rows of 1..4 16-byte chunks per thread (N 8..8192 in multiples of 8),
+    the element-load kernel past those (N 8200, N 100), weights of x's dtype or
+    fp32, and a row start that is only 2-byte aligned (element-load kernel),
+    all against the oracle."""
+    from src import _lib
+    from src.rms_norm import rmsnorm_triton
+    g = torch.Generator("cpu").manual_seed(N)
+    x = (torch.randn(5, N, generator=g) * 2).to(dtype).to(dev)
+    w = (torch.rand(N, generator=g) + 0.5).to(wdtype).to(dev)
+    ref = oq.rmsnorm(x, w, 1e-6)
+    tol = (2e-2 if dtype == torch.bfloat16 else 2e-3) * float(ref.float().abs().max())
+    y = rmsnorm_triton(x, w, 1e-6)
+    assert max_abs(y, ref) < tol
+    # rows starting one element into the allocation
+    buf = torch.empty(5 * N + 1, dtype=dtype, device=dev)
+    xs = buf[1:].view(5, N)
+    xs.copy_(x)
+    ys = torch.empty_like(x)
+    st = _lib.load().mi_rmsnorm(xs.data_ptr(), w.data_ptr(), ys.data_ptr(), 5, N, N, N, 1e-6,
+                                _lib.dtype_code(dtype), _lib.dtype_code(wdtype), _lib.stream_of(x))
+    _lib.check(st, "rmsnorm")
+    assert max_abs(ys, ref) < tol
+
+
 @pytest.mark.parametrize("M,K,N", [(1, 2048, 2048), (1, 8192, 2048), (8, 2048, 2048),
                                    (16, 1024, 512), (24, 2048, 1024), (3, 80, 100)])
 def test_w8a16_gemv_kernel_and_small_m_route(dev, M, K, N):
