@@ -17,6 +17,10 @@
 //     through LDS;
 //   * no MFMA: at one query token per head there is nothing to amortise a
 //     matrix tile over, and the loop is HBM-bound;
+//   * grids of at most one block per CU (2-byte K/V, whole-chunk rows) run a
+//     software pipeline over two register sets: the next pass's K/V loads are
+//     in flight while the current pass is folded in (PIPE, 4 waves, 512-thread
+//     register budget); larger grids overlap their blocks instead;
 //   * all splits of one (batch, kv-head) group run on one XCD (the hardware
 //     deals workgroup i to XCD i mod n_xcc), so with an arrival counter the
 //     last split of a group can combine the group's partials from that XCD's
@@ -339,8 +343,8 @@ __device__ inline void combine_row_wave(const CombineArgs& a, int64_t bh, int la
 // different key offsets (the same offsets at once alias HBM channels: 8
 // groups x 128 splits ran 110 us in step, 92 rotated).  Padding blocks
 // (groups past the last) exit at once.
-template <typename T, int P, int GC, bool MASK, int MODE, bool FUSED>
-__global__ __launch_bounds__((split_max_threads<T, P, GC, MASK>())) void decode_split_kernel(DecodeArgs a) {
+template <typename T, int P, int GC, bool MASK, int MODE, bool FUSED, bool PIPE = false>
+__global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>())) void decode_split_kernel(DecodeArgs a) {
   using Geo = DecodeGeom<T, P>;
   constexpr int EPC = Geo::kEPC, LPR = Geo::kLPR, CPL = Geo::kCPL,
                 E = Geo::kE, RPW = Geo::kRPW, U = Geo::kU;
@@ -462,10 +466,12 @@ __global__ __launch_bounds__((split_max_threads<T, P, GC, MASK>())) void decode_
   // groups runs in one-group passes (so a split just past a multiple of the
   // U-group step does not pay a whole U-group pass for a few keys), a longer
   // one in one more U-group pass (one round trip instead of up to U).
-  auto pass = [&](auto uu_c, const int base, const int wbase, const int wend)
-      __attribute__((always_inline)) {
+  // load_rows issues the K and V loads of the UU row groups from `base`;
+  // compute_rows folds them into the running softmax.
+  auto load_rows = [&](auto uu_c, const int base, const int wbase, const int wend,
+                       u32x4 (&kr)[decltype(uu_c)::value][CPL],
+                       u32x4 (&vr)[decltype(uu_c)::value][CPL]) __attribute__((always_inline)) {
     constexpr int UU = decltype(uu_c)::value;
-    u32x4 kr[UU][CPL], vr[UU][CPL];
     int row[UU];
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
@@ -496,6 +502,16 @@ __global__ __launch_bounds__((split_max_threads<T, P, GC, MASK>())) void decode_
 #pragma unroll
       for (int j = 0; j < CPL; ++j)
         vr[u][j] = load_chunk(vb + rl * a.v_sl + j * LPR * EPC, j);
+    }
+  };
+  auto compute_rows = [&](auto uu_c, const int base, const int wbase, const int wend,
+                          u32x4 (&kr)[decltype(uu_c)::value][CPL],
+                          u32x4 (&vr)[decltype(uu_c)::value][CPL]) __attribute__((always_inline)) {
+    constexpr int UU = decltype(uu_c)::value;
+    int row[UU];
+#pragma unroll
+    for (int u = 0; u < UU; ++u) {
+      row[u] = base + u * nw * RPW + my_off;
     }
 
     float s[UU][GC];
@@ -549,10 +565,43 @@ __global__ __launch_bounds__((split_max_threads<T, P, GC, MASK>())) void decode_
         for (int e = 0; e < E; ++e) acc[g][e] = fmaf(p[u][g], vf[e], acc[g][e]);
     }
   };
+  auto pass = [&](auto uu_c, const int base, const int wbase, const int wend)
+      __attribute__((always_inline)) {
+    constexpr int UU = decltype(uu_c)::value;
+    u32x4 kr[UU][CPL], vr[UU][CPL];
+    load_rows(uu_c, base, wbase, wend, kr, vr);
+    compute_rows(uu_c, base, wbase, wend, kr, vr);
+  };
   const int rows_per_group = nw * RPW, step = U * rows_per_group;
-  // the split in windows of kMaskWin rows with a mask (one window without)
-  auto run_window = [&](const int wbase, const int wend) __attribute__((always_inline)) {
-    int base = wbase;
+  // rows [first, wend) of the window staged from wbase (the split in windows of
+  // kMaskWin rows with a mask, one window without)
+  auto run_window = [&](const int wbase, const int first, const int wend)
+      __attribute__((always_inline)) {
+    if constexpr (PIPE) {
+      // Software pipeline over two register sets: the loads of the next U-group
+      // pass are issued before the current pass is folded in, so a split costs
+      // one round trip plus its stream instead of a round trip per pass.  Both
+      // sets are named statically (the loop body is unrolled twice) so no
+      // register copy waits on a load in flight; every prefetch covers at least
+      // one row below wend, and the last pass's rows past wend are dropped.
+      if (first >= wend) return;
+      constexpr auto uc = std::integral_constant<int, U>{};
+      u32x4 ka[U][CPL], va[U][CPL], kb2[U][CPL], vb2[U][CPL];
+      int base = first;
+      load_rows(uc, base, wbase, wend, ka, va);
+      while (true) {
+        if (base + step >= wend) { compute_rows(uc, base, wbase, wend, ka, va); break; }
+        load_rows(uc, base + step, wbase, wend, kb2, vb2);
+        compute_rows(uc, base, wbase, wend, ka, va);
+        base += step;
+        if (base + step >= wend) { compute_rows(uc, base, wbase, wend, kb2, vb2); break; }
+        load_rows(uc, base + step, wbase, wend, ka, va);
+        compute_rows(uc, base, wbase, wend, kb2, vb2);
+        base += step;
+      }
+      return;
+    }
+    int base = first;
     for (; base + step <= wend; base += step)
       pass(std::integral_constant<int, U>{}, base, wbase, wend);
     if (wend - base > 2 * rows_per_group) {
@@ -566,13 +615,53 @@ __global__ __launch_bounds__((split_max_threads<T, P, GC, MASK>())) void decode_
     for (int wbase = start; wbase < end; wbase += kMaskWin) {
       const int wend = min(wbase + kMaskWin, end);
       __syncthreads();  // the previous window's mask reads are done
-      for (int i = tid; i < wend - wbase; i += blockDim.x)
-        msk[i] = mb[(int64_t)(wbase + i) * a.mask_sl] != 0;
+      // 16 consecutive rows per thread, all 16 byte loads issued before the
+      // first use (one round trip per 16 * blockDim rows; a 4096-row window
+      // in one pass at 256 threads or more); rows past wend re-read the last
+      // row and are never selected.  The first and last selected rows of the
+      // window bound the rows streamed: a padding mask (keys j < L_b) costs
+      // the keys it selects, not the cache capacity.
+      const int n = wend - wbase;
+      int lo = n, hi = -1;
+      for (int c = tid * 16; c < n; c += blockDim.x * 16) {
+        unsigned char mv[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          mv[e] = mb[(int64_t)min(wbase + c + e, wend - 1) * a.mask_sl];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          if (mv[e] != 0 && c + e < n) {
+            lo = min(lo, c + e);
+            hi = max(hi, c + e);
+          }
+        }
+        uint32_t* dst = reinterpret_cast<uint32_t*>(msk + c);
+#pragma unroll
+        for (int wd = 0; wd < 4; ++wd)
+          dst[wd] = (uint32_t)(mv[4 * wd] != 0) | ((uint32_t)(mv[4 * wd + 1] != 0) << 8) |
+                    ((uint32_t)(mv[4 * wd + 2] != 0) << 16) |
+                    ((uint32_t)(mv[4 * wd + 3] != 0) << 24);
+      }
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) {
+        lo = min(lo, __shfl_xor(lo, off));
+        hi = max(hi, __shfl_xor(hi, off));
+      }
+      int* bnd = reinterpret_cast<int*>(msk + kMaskWin);   // [nw] lo, [nw] hi
+      if (lane == 0) {
+        bnd[w] = lo;
+        bnd[nw + w] = hi;
+      }
       __syncthreads();
-      run_window(wbase, wend);
+      int wlo = n, whi = -1;
+      for (int ww = 0; ww < nw; ++ww) {
+        wlo = min(wlo, bnd[ww]);
+        whi = max(whi, bnd[nw + ww]);
+      }
+      if (whi >= 0) run_window(wbase, wbase + wlo, wbase + whi + 1);
     }
   } else {
-    run_window(start, end);
+    run_window(start, start, end);
   }
 
   // Merge the RPW row groups of this wave (butterfly over lane strides).
@@ -829,14 +918,47 @@ struct DecodePlan {
   int n_xcc, n_groups;
   int P, mode;
   bool fused;   // in-launch combine (MODE 0, no mask; a.arrive set)
+  bool pipe;    // software-pipelined passes (2-byte MODE 0; at most 8 waves)
 };
+
+template <typename T, int P, int GC, int MODE>
+hipError_t launch_split_unpiped(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream);
 
 template <typename T, int P, int GC, int MODE>
 hipError_t launch_split_t(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
   const int S = a.num_splits;
+  if constexpr (MODE == 0 && sizeof(T) == 2) {
+    // 2-byte K/V with whole-chunk rows: the software-pipelined kernels when
+    // the plan asks for them
+    if (!p.pipe) return launch_split_unpiped<T, P, GC, MODE>(a, p, stream);
+    const int nw = min(p.nw, 8);   // built for at most 512 threads
+    const size_t shmem = (size_t)nw * GC * (P + 2) * sizeof(float);
+    const dim3 grid((unsigned)(p.n_groups * S));
+    if (a.mask != nullptr) {
+      hipLaunchKernelGGL((decode_split_kernel<T, P, GC, true, 0, false, true>), grid,
+                         dim3((unsigned)(nw * 64)), shmem + kMaskWin + 8 * nw, stream, a);
+    } else if (p.fused) {
+      const int per_xcc = (p.n_groups + p.n_xcc - 1) / p.n_xcc;
+      hipLaunchKernelGGL((decode_split_kernel<T, P, GC, false, 0, true, true>),
+                         dim3((unsigned)(p.n_xcc * per_xcc * S)), dim3((unsigned)(nw * 64)),
+                         shmem, stream, a);
+    } else {
+      hipLaunchKernelGGL((decode_split_kernel<T, P, GC, false, 0, false, true>), grid,
+                         dim3((unsigned)(nw * 64)), shmem, stream, a);
+    }
+    return hipGetLastError();
+  } else {
+    return launch_split_unpiped<T, P, GC, MODE>(a, p, stream);
+  }
+}
+
+// One pass of loads in flight per wave, up to 16 waves per block.
+template <typename T, int P, int GC, int MODE>
+hipError_t launch_split_unpiped(const DecodeArgs& a, const DecodePlan& p, hipStream_t stream) {
+  const int S = a.num_splits;
   if (a.mask != nullptr) {
     const int nw = min(p.nw, split_max_threads<T, P, GC, true>() / 64);
-    const size_t shmem = (size_t)nw * GC * (P + 2) * sizeof(float) + kMaskWin;
+    const size_t shmem = (size_t)nw * GC * (P + 2) * sizeof(float) + kMaskWin + 8 * nw;
     hipLaunchKernelGGL((decode_split_kernel<T, P, GC, true, MODE, false>),
                        dim3((unsigned)(p.n_groups * S)), dim3((unsigned)(nw * 64)), shmem, stream,
                        a);

@@ -234,6 +234,28 @@ def test_mask_excluded_rows_are_not_read(dev, D, L, splits):
     assert max_abs(lse.cpu()[~empty], ref_lse[~empty]) < LSE_TOL
 
 
+@pytest.mark.parametrize("splits", [1, 3])
+def test_mask_window_bounds(dev, splits):
+    """Each 4096-row mask window streams only rows between its first and last
+    selected key: runs that end on a window boundary, start and end inside
+    windows, a single selected key at a window start, and a run through the
+    last row, with NaN in every row the mask excludes."""
+    B, Hq, Hkv, L, D = 4, 8, 2, 9000, 128
+    q, k, v = _inputs(B, Hq, Hkv, L, D, torch.bfloat16, dev, seed=31)
+    mask = torch.zeros((B, L), dtype=torch.bool)
+    for b, (lo, hi) in enumerate([(0, 4096), (100, 4200), (4096, 4097), (8191, 9000)]):
+        mask[b, lo:hi] = True
+    kc, vc = k.clone(), v.clone()
+    keep = mask.to(dev)[:, None, :, None]
+    k = torch.where(keep, k, torch.full_like(k, float("nan")))
+    v = torch.where(keep, v, torch.full_like(v, float("nan")))
+    out, lse = _fd()(q, k, v, mask=mask.to(dev), num_splits=splits, return_lse=True)
+    assert not torch.isnan(out).any()
+    ref, ref_lse = ora.decode(q, kc, vc, mask=mask)
+    assert max_abs(out, ref) < 2e-2
+    assert max_abs(lse, ref_lse) < LSE_TOL
+
+
 @pytest.mark.parametrize("B", [2, 3, 64, 65])
 def test_seq_lens_rows_dealt_by_length(dev, B):
     """With seq_lens and 2 <= B <= 64 the split kernel deals its grid rows by
