@@ -732,7 +732,14 @@ hipError_t dispatch_dg_k(const LayerGemvArgs& a, int n_blocks, hipStream_t st) {
     case 512: return launch_dg<T, NORM, EPI, TPB, 4, 1>(a, n_blocks, st);
     case 1024: return launch_dg<T, NORM, EPI, TPB, 8, 1>(a, n_blocks, st);
     case 1536: return launch_dg<T, NORM, EPI, TPB, 12, 1>(a, n_blocks, st);
-    case 2048: return launch_dg<T, NORM, EPI, TPB, 16, 1>(a, n_blocks, st);
+    // K = 2048 (the 1B model's projections from the residual stream): fewer,
+    // longer waves pay the per-wave set-up, RMSNorm statistics and cross-wave
+    // reduction less often.  One MI355X, M = 8, per call in a 16-layer graph:
+    // wo + residual 4.03 -> 3.75 us (16 x 1 -> 4 x 4), w1|w3 + SwiGLU 11.2 ->
+    // 9.9 us (8 x 2), RMSNorm + QKV + RoPE + append about 0.85 us less (4 x 4).
+    case 2048:
+      if constexpr (EPI == kEpiSwiglu) return launch_dg<T, NORM, EPI, TPB, 8, 2>(a, n_blocks, st);
+      else return launch_dg<T, NORM, EPI, TPB, 4, 4>(a, n_blocks, st);
     case 3072: return launch_dg<T, NORM, EPI, TPB, 12, 2>(a, n_blocks, st);
     case 4096: return launch_dg<T, NORM, EPI, TPB, 16, 2>(a, n_blocks, st);
     default: break;
