@@ -61,15 +61,20 @@ bool supported_head_dim(int64_t D) { return D >= 1 && D <= 256; }
 // Load mode for a head_dim and K/V layout: 0 = head_dim is the power of two
 // P and rows are 16-byte aligned; 1 = head_dim fills whole 16-byte chunks of
 // aligned rows (lanes past it load nothing); 2 = element loads (any head_dim,
-// any element-aligned rows).
+// any element-aligned rows, row strides past 512 KB).
 int load_mode(int32_t dtype, int64_t D, const void* k, const void* v, int64_t k_sb,
               int64_t k_sh, int64_t k_sl, int64_t v_sb, int64_t v_sh, int64_t v_sl) {
   const int64_t eb = elem_bytes(dtype);
   const bool aligned = ((uintptr_t)k % 16) == 0 && ((uintptr_t)v % 16) == 0 &&
                        (k_sb * eb) % 16 == 0 && (k_sh * eb) % 16 == 0 && (k_sl * eb) % 16 == 0 &&
                        (v_sb * eb) % 16 == 0 && (v_sh * eb) % 16 == 0 && (v_sl * eb) % 16 == 0;
-  if (aligned && D == pad_dim(D)) return 0;
-  if (aligned && (D * eb) % 16 == 0) return 1;
+  // MODE 0/1 address a pass's rows by 32-bit offsets from the pass's first
+  // row: at most 4096 rows (16 waves x 64 rows x 4) of the larger row stride
+  // stay below the out-of-range offset
+  const int64_t max_rb = std::max(k_sl, v_sl) * eb;
+  const bool span_ok = max_rb * 4096 + 256 * 4 < (int64_t)kOobOffset;
+  if (aligned && span_ok && D == pad_dim(D)) return 0;
+  if (aligned && span_ok && (D * eb) % 16 == 0) return 1;
   return 2;
 }
 

@@ -423,7 +423,6 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
       }
     }
   }
-
   float m[GC], l[GC], acc[GC][E];
 #pragma unroll
   for (int g = 0; g < GC; ++g) {
@@ -437,6 +436,16 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
                 (int64_t)kvh * a.k_sh + li * EPC;
   const T* vb = reinterpret_cast<const T*>(a.v) + (int64_t)b * a.v_sb +
                 (int64_t)kvh * a.v_sh + li * EPC;
+  // MODE 0/1 rows through buffer resources: one resource per pass at the
+  // pass's first row (scalar arithmetic); each lane's byte offset of row slot
+  // u within a pass is fixed, and rows past the window (or excluded by a mask)
+  // get an out-of-range offset: zeros, no memory access.  The host keeps a
+  // pass's span (step rows x row stride + a row) below kOobOffset.
+  const int64_t k_rb = a.k_sl * (int64_t)sizeof(T), v_rb = a.v_sl * (int64_t)sizeof(T);
+  const unsigned char* k_slab = reinterpret_cast<const unsigned char*>(a.k) +
+                                ((int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh) * (int64_t)sizeof(T);
+  const unsigned char* v_slab = reinterpret_cast<const unsigned char*>(a.v) +
+                                ((int64_t)b * a.v_sb + (int64_t)kvh * a.v_sh) * (int64_t)sizeof(T);
   const uint8_t* mb = MASK ? a.mask + (int64_t)b * a.mask_sb : nullptr;
   const int my_off = w * RPW + rg;
   // With a mask, the bytes of the current window of rows are staged in LDS
@@ -477,11 +486,45 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
     for (int u = 0; u < UU; ++u) {
       row[u] = base + u * nw * RPW + my_off;
     }
-    // Rows past the window re-read the window's last row (always in bounds,
-    // never a key beyond seq_lens: a cache hit, not a stream) and are dropped
-    // from the softmax below; with a mask, so are the rows it excludes (2-byte
-    // K/V; fp32 keeps the plain clamp, the 1024-thread kernels have no
-    // registers to spare for the row selection).
+    if constexpr (MODE != 2) {
+      // (every term is wave-uniform; readfirstlane keeps the resources scalar)
+      const int ub = __builtin_amdgcn_readfirstlane(base);
+      const buf_rsrc krs = make_rsrc(uniform_ptr(k_slab + (int64_t)ub * k_rb), kOobOffset);
+      const buf_rsrc vrs = make_rsrc(uniform_ptr(v_slab + (int64_t)ub * v_rb), kOobOffset);
+      bool ok[UU];
+#pragma unroll
+      for (int u = 0; u < UU; ++u) {
+        ok[u] = row[u] < wend;
+        if constexpr (MASK) ok[u] = ok[u] && msk[row[u] - wbase] != 0;
+      }
+      // every K load before any V load: the scores need only K, so the
+      // first wait leaves the V stream in flight
+#pragma unroll
+      for (int u = 0; u < UU; ++u) {
+        const int rs = u * nw * RPW + my_off;    // row slot within the pass
+        const uint32_t ko = ok[u] ? (uint32_t)(rs * k_rb) + (uint32_t)(li * 16) : kOobOffset;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          kr[u][j] = (MODE == 1 && !cvalid[j]) ? u32x4{0u, 0u, 0u, 0u}
+                                               : buf_load16_nt(krs, ko + (uint32_t)(j * LPR * 16));
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < UU; ++u) {
+        const int rs = u * nw * RPW + my_off;
+        const uint32_t vo = ok[u] ? (uint32_t)(rs * v_rb) + (uint32_t)(li * 16) : kOobOffset;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          vr[u][j] = (MODE == 1 && !cvalid[j]) ? u32x4{0u, 0u, 0u, 0u}
+                                               : buf_load16_nt(vrs, vo + (uint32_t)(j * LPR * 16));
+        }
+      }
+      return;
+    }
+    // MODE 2: rows past the window re-read the window's last row (always in
+    // bounds, never a key beyond seq_lens: a cache hit, not a stream) and are
+    // dropped from the softmax below; with a mask, so are the rows it
+    // excludes (2-byte K/V; fp32 keeps the plain clamp).
     auto src_row = [&](const int r) __attribute__((always_inline)) -> int64_t {
       int x = min(r, wend - 1);
       if constexpr (sizeof(T) == 2 && MASK) {
@@ -519,8 +562,9 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
     for (int u = 0; u < UU; ++u) {
       bool keep = row[u] < wend;
       if (MASK && keep) keep = msk[row[u] - wbase] != 0;
-      // a stand-in row adds exactly zero (its V is not a key of this row)
-      if (sizeof(T) == 2 && MASK && !keep) {
+      // a stand-in row adds exactly zero (its V is not a key of this row; the
+      // buffer loads of MODE 0/1 already read zeros)
+      if (MODE == 2 && sizeof(T) == 2 && MASK && !keep) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j) vr[u][j] = u32x4{0u, 0u, 0u, 0u};
       }

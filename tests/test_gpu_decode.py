@@ -234,6 +234,23 @@ def test_mask_excluded_rows_are_not_read(dev, D, L, splits):
     assert max_abs(lse.cpu()[~empty], ref_lse[~empty]) < LSE_TOL
 
 
+def test_row_stride_past_buffer_span(dev):
+    """K/V rows 600 KB apart (a view into a larger cache): past the span the
+    buffer-offset loads cover, the element-load path serves the call."""
+    B, Hq, Hkv, L, D, stride = 1, 4, 1, 40, 64, 300_000
+    g = torch.Generator().manual_seed(41)
+    q = torch.randn((B, Hq, 1, D), generator=g).to(torch.bfloat16).to(dev)
+    kbuf = torch.randn((L * stride,), generator=g).to(torch.bfloat16).to(dev)
+    vbuf = torch.randn((L * stride,), generator=g).to(torch.bfloat16).to(dev)
+    k = kbuf.as_strided((B, Hkv, L, D), (L * stride, L * stride, stride, 1))
+    v = vbuf.as_strided((B, Hkv, L, D), (L * stride, L * stride, stride, 1))
+    for splits in (1, 4):
+        out, lse = _fd()(q, k, v, num_splits=splits, return_lse=True)
+        ref, ref_lse = ora.decode(q, k.contiguous(), v.contiguous())
+        assert max_abs(out, ref) < 2e-2
+        assert max_abs(lse, ref_lse) < LSE_TOL
+
+
 @pytest.mark.parametrize("splits", [1, 3])
 def test_mask_window_bounds(dev, splits):
     """Each 4096-row mask window streams only rows between its first and last
