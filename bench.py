@@ -193,8 +193,13 @@ def bench_decode_cfg4(torch, steps: int, warmup: int) -> dict:
     ks = [torch.randn((1, 8, 131072, 128), generator=g).to(torch.bfloat16).to(dev) for _ in range(n_sets)]
     vs = [torch.randn((1, 8, 131072, 128), generator=g).to(torch.bfloat16).to(dev) for _ in range(n_sets)]
     nbytes = 131072 * 8 * 128 * 2 * 2 + 2 * 24 * 128 * 2
-    sweep = {}
+    from src import _lib
+    sweep, ranges = {}, {}
     for splits in (16, 32, 64, 128):
+        # the key ranges the library runs for this request (too few splits to
+        # fill the CUs are subdivided: 16 requested -> 32 ranges here)
+        ranges[str(splits)] = int(_lib.load().mi_decode_effective_splits(1, 24, 8, 131072, 128,
+                                                                         splits))
         graph = _graph_decode(
             torch, lambda i, s=splits: flash_decode(qs[i], ks[i], vs[i], num_splits=s), n_sets)
         ms = _time_graph(torch, graph, n_sets, max(steps, 20), warmup)
@@ -203,6 +208,7 @@ def bench_decode_cfg4(torch, steps: int, warmup: int) -> dict:
     best = max(sweep.values())
     out = {"config": "4: decode B1 L131072 24/8 D128, splits sweep (combine included)",
            "unit": "GB/s", "by_splits": sweep, "value": best,
+           "key_ranges_by_splits": ranges,
            "roofline": {"bound": "hbm", "achieved": best, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(best / HBM_PEAK_GBS, 4),
                         "traffic": _traffic("decode_config3_4_traffic.md",
@@ -534,8 +540,8 @@ def cpu_baselines(torch) -> dict:
 
 def bench_prefill_d128(torch, steps: int, warmup: int) -> dict:
     """Causal GQA prefill at the Llama-3.2-3B head shape of configs 3 and 4
-    (B4 S2048 24/8 heads D128, bf16, fp32 LSE): prefill_kernel<128>, one
-    launch per step, timed as the headline leg is."""
+    (B4 S2048 24/8 heads D128, bf16, fp32 LSE): prefill_sp2_kernel<bf16,128>,
+    one launch per step, timed as the headline leg is."""
     from src.flash_attn import flash_attention
     dev = torch.device("cuda:0")
     B, Hq, Hkv, S, D = 4, 24, 8, 2048, 128
@@ -558,7 +564,7 @@ def bench_prefill_d128(torch, steps: int, warmup: int) -> dict:
     return {"config": "causal GQA prefill B4 S2048 Hq24 Hkv8 D128 (the 3B head shape of configs "
                       "3/4), bf16, fp32 LSE",
             "value": round(achieved, 1), "unit": "TFLOP/s", "ms_per_step": ms, "flops": flops,
-            "roofline": {"bound": "mfma", "kernel": "prefill_kernel<128>",
+            "roofline": {"bound": "mfma", "kernel": "prefill_sp2_kernel<bf16,128>",
                          "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(achieved / BF16_PEAK_TFLOPS, 4),
                          "traffic": _traffic("prefill_d128_traffic.md", "hbm_bytes_per_launch")}}
