@@ -158,6 +158,11 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a) {
   }
 }
 
+// The cache rows are written with non-temporal stores (streamed to memory
+// rather than kept in L2): at config 2's model-layout prefill (33.5 MB moved)
+// 7.5 -> 7.0 us per call, and the attention block that then reads the cache
+// 88.7 -> 87.4 us (one MI355X).  The inputs keep temporal loads: they are the
+// projection outputs just written, and non-temporal loads of them cost 11 us.
 template <typename T>
 __global__ __launch_bounds__(256) void rope_kv_append_vec_kernel(KvAppendArgs a) {
   const uint32_t nj = (uint32_t)a.half >> 3, per_row = (uint32_t)a.S * nj;
@@ -180,14 +185,14 @@ __global__ __launch_bounds__(256) void rope_kv_append_vec_kernel(KvAppendArgs a)
         const T* sp = reinterpret_cast<const T*>(a.sin) + crow * a.s_ss + i0;
         u32x4 ya, yb;
         rotate8<T>(k1, k2, load16(cp), load16(sp), ya, yb);
-        *reinterpret_cast<u32x4*>(kc) = ya;
-        *reinterpret_cast<u32x4*>(kc + a.half) = yb;
+        __builtin_nontemporal_store(ya, reinterpret_cast<u32x4*>(kc));
+        __builtin_nontemporal_store(yb, reinterpret_cast<u32x4*>(kc + a.half));
       } else {  // plain KV write: K copied bitwise too
-        *reinterpret_cast<u32x4*>(kc) = k1;
-        *reinterpret_cast<u32x4*>(kc + a.half) = k2;
+        __builtin_nontemporal_store(k1, reinterpret_cast<u32x4*>(kc));
+        __builtin_nontemporal_store(k2, reinterpret_cast<u32x4*>(kc + a.half));
       }
-      *reinterpret_cast<u32x4*>(vc) = v1;
-      *reinterpret_cast<u32x4*>(vc + a.half) = v2;
+      __builtin_nontemporal_store(v1, reinterpret_cast<u32x4*>(vc));
+      __builtin_nontemporal_store(v2, reinterpret_cast<u32x4*>(vc + a.half));
     }
   }
 }
