@@ -179,8 +179,14 @@ def test_graph_runner_takes_a_reference_style_model(dev):
         kv.v.copy_(snap_v)
         b = nat_runner.decode(tok, pos).clone()
         torch.cuda.synchronize()
-        # same slot contents; logits through the mask path vs seq_lens within the bar
-        assert torch.equal(ka, kv.k) and torch.equal(va, kv.v)
+        # same slots; layer 0 sees identical inputs -> identical contents.
+        # Deeper layers may differ in the last bits: the mask path splits the
+        # cache capacity and the seq_lens path each sequence's own length, so
+        # the per-split maxima (and the rounding of p) differ.  Logits within
+        # the bar.
+        assert torch.equal(ka[0], kv.k[0]) and torch.equal(va[0], kv.v[0])
+        assert max_abs(ka, kv.k) < 2e-2 * float(kv.k.abs().max())
+        assert max_abs(va, kv.v) < 2e-2 * float(kv.v.abs().max())
         _logit_check(a, b)
         snap_k, snap_v = kv.k.clone(), kv.v.clone()
         pos += 1
