@@ -42,6 +42,24 @@ def test_decode_matches_oracle(dev, dtype, D, Hq, Hkv):
     assert max_abs(lse, ref_lse) < LSE_TOL
 
 
+@pytest.mark.parametrize("dtype,u", [(torch.bfloat16, 2.0 ** -8), (torch.float16, 2.0 ** -11)])
+@pytest.mark.parametrize("D,Hq,Hkv,B,L", [(64, 32, 8, 8, 4097), (128, 24, 8, 3, 777)])
+@pytest.mark.parametrize("q_scale", [0.1, 1.0, 8.0])
+def test_pv_rounding_bound(dev, dtype, u, D, Hq, Hkv, B, L, q_scale):
+    """2-byte K/V fold P.V with each p rounded to the storage type (unit
+    roundoff u) and the output rounded once more, so against the fp32 oracle
+    |out - ref| <= 2u * max|v| for flat (q_scale 0.1) to peaked (8.0) softmax
+    rows, with V of unit and of larger (x 16) magnitude."""
+    q, k, v = _inputs(B, Hq, Hkv, L, D, dtype, dev, seed=41)
+    q = (q.float() * q_scale).to(dtype)
+    for vs in (1.0, 16.0):
+        vv = (v.float() * vs).to(dtype)
+        out = _fd()(q, k, vv)
+        ref, _ = ora.decode(q, k, vv)
+        bound = 2 * u * float(vv.abs().max()) + 1e-6
+        assert max_abs(out, ref) <= bound, (vs, max_abs(out, ref), bound)
+
+
 @pytest.mark.parametrize("num_splits", [1, 2, 7, 16, 64, 200])
 def test_split_count_invariance(dev, num_splits):
     q, k, v = _inputs(2, 24, 8, 3001, 128, torch.bfloat16, dev, seed=5)
