@@ -526,7 +526,9 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
 #pragma unroll
       for (int u = 0; u < UU; ++u) {
         ok[u] = row[u] < wend;
-        if constexpr (MASK) ok[u] = ok[u] && msk[min(row[u] - wbase, kMaskWin - 1)] != 0;
+        // & (not &&): the clamped LDS read is always in bounds, and without the
+        // short circuit the selection needs no branch in the pass
+        if constexpr (MASK) ok[u] = ok[u] & (msk[min(row[u] - wbase, kMaskWin - 1)] != 0);
       }
       // every K load before any V load: the scores need only K, so the
       // first wait leaves the V stream in flight
@@ -559,7 +561,7 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
     auto src_row = [&](const int r) __attribute__((always_inline)) -> int64_t {
       int x = min(r, wend - 1);
       if constexpr (sizeof(T) == 2 && MASK) {
-        if (r < wend && msk[min(r - wbase, kMaskWin - 1)] == 0) x = wend - 1;
+        if ((r < wend) & (msk[min(r - wbase, kMaskWin - 1)] == 0)) x = wend - 1;
       }
       return x;
     };
@@ -592,7 +594,7 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
       bool keep = row[u] < wend;
-      if (MASK && keep) keep = msk[min(row[u] - wbase, kMaskWin - 1)] != 0;
+      if constexpr (MASK) keep = keep & (msk[min(row[u] - wbase, kMaskWin - 1)] != 0);
       // a stand-in row adds exactly zero (its V is not a key of this row; the
       // buffer loads of MODE 0/1 already read zeros)
       if (MODE == 2 && sizeof(T) == 2 && MASK && !keep) {
