@@ -469,9 +469,11 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
                 (int64_t)kvh * a.v_sh + li * EPC;
   // MODE 0/1 rows through buffer resources: one resource per pass at the
   // pass's first row (scalar arithmetic); each lane's byte offset of row slot
-  // u within a pass is fixed, and rows past the window (or excluded by a mask)
-  // get an out-of-range offset: zeros, no memory access.  The host keeps a
-  // pass's span (step rows x row stride + a row) below kOobOffset.
+  // u within a pass is fixed.  Without a mask the resource ends at the
+  // window's last row, so rows past it read zeros with no memory access at
+  // those same offsets; with a mask, rows past the window or excluded by it
+  // get an out-of-range offset instead.  The host keeps a pass's span (step
+  // rows x row stride + a row) below kOobOffset.
   const int64_t k_rb = a.k_sl * (int64_t)sizeof(T), v_rb = a.v_sl * (int64_t)sizeof(T);
   const unsigned char* k_slab = reinterpret_cast<const unsigned char*>(a.k) +
                                 ((int64_t)b * a.k_sb + (int64_t)kvh * a.k_sh) * (int64_t)sizeof(T);
@@ -520,15 +522,26 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
     if constexpr (MODE != 2) {
       // (every term is wave-uniform; readfirstlane keeps the resources scalar)
       const int ub = __builtin_amdgcn_readfirstlane(base);
-      const buf_rsrc krs = make_rsrc(uniform_ptr(k_slab + (int64_t)ub * k_rb), kOobOffset);
-      const buf_rsrc vrs = make_rsrc(uniform_ptr(v_slab + (int64_t)ub * v_rb), kOobOffset);
+      // without a mask the resources end at wend's row, so rows at or past it
+      // fall outside them (zeros, no memory access) at their fixed offsets:
+      // no per-pass offset selection
+      uint32_t kn = kOobOffset, vn = kOobOffset;
+      if constexpr (!MASK) {
+        const int64_t rows_left = (int64_t)__builtin_amdgcn_readfirstlane(wend) - ub;
+        const int64_t kb_ = rows_left * k_rb, vb_ = rows_left * v_rb;
+        kn = (uint32_t)(kb_ <= 0 ? 0 : (kb_ < (int64_t)kOobOffset ? kb_ : (int64_t)kOobOffset));
+        vn = (uint32_t)(vb_ <= 0 ? 0 : (vb_ < (int64_t)kOobOffset ? vb_ : (int64_t)kOobOffset));
+      }
+      const buf_rsrc krs = make_rsrc(uniform_ptr(k_slab + (int64_t)ub * k_rb), kn);
+      const buf_rsrc vrs = make_rsrc(uniform_ptr(v_slab + (int64_t)ub * v_rb), vn);
       bool ok[UU];
 #pragma unroll
       for (int u = 0; u < UU; ++u) {
-        ok[u] = row[u] < wend;
+        ok[u] = true;
         // & (not &&): the clamped LDS read is always in bounds, and without the
         // short circuit the selection needs no branch in the pass
-        if constexpr (MASK) ok[u] = ok[u] & (msk[min(row[u] - wbase, kMaskWin - 1)] != 0);
+        if constexpr (MASK)
+          ok[u] = (row[u] < wend) & (msk[min(row[u] - wbase, kMaskWin - 1)] != 0);
       }
       // every K load before any V load: the scores need only K, so the
       // first wait leaves the V stream in flight
@@ -580,10 +593,13 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
         vr[u][j] = load_chunk(vb + rl * a.v_sl + j * LPR * EPC, j);
     }
   };
-  auto compute_rows = [&](auto uu_c, const int base, const int wbase, const int wend,
+  // full_c: every row of the pass is below wend (a pass of the loop body, not
+  // the window's last), so only a mask can drop one
+  auto compute_rows = [&](auto uu_c, auto full_c, const int base, const int wbase, const int wend,
                           u32x4 (&kr)[decltype(uu_c)::value][CPL],
                           u32x4 (&vr)[decltype(uu_c)::value][CPL]) __attribute__((always_inline)) {
     constexpr int UU = decltype(uu_c)::value;
+    constexpr bool FULL = decltype(full_c)::value;
     int row[UU];
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
@@ -593,7 +609,7 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
     float s[UU][GC];
 #pragma unroll
     for (int u = 0; u < UU; ++u) {
-      bool keep = row[u] < wend;
+      bool keep = FULL || row[u] < wend;
       if constexpr (MASK) keep = keep & (msk[min(row[u] - wbase, kMaskWin - 1)] != 0);
       // a stand-in row adds exactly zero (its V is not a key of this row; the
       // buffer loads of MODE 0/1 already read zeros)
@@ -670,12 +686,12 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
       }
     }
   };
-  auto pass = [&](auto uu_c, const int base, const int wbase, const int wend)
+  auto pass = [&](auto uu_c, auto full_c, const int base, const int wbase, const int wend)
       __attribute__((always_inline)) {
     constexpr int UU = decltype(uu_c)::value;
     u32x4 kr[UU][CPL], vr[UU][CPL];
     load_rows(uu_c, base, wbase, wend, kr, vr);
-    compute_rows(uu_c, base, wbase, wend, kr, vr);
+    compute_rows(uu_c, full_c, base, wbase, wend, kr, vr);
   };
   const int rows_per_group = nw * RPW, step = U * rows_per_group;
   // rows [first, wend) of the window staged from wbase (the split in windows of
@@ -695,25 +711,25 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
       int base = first;
       load_rows(uc, base, wbase, wend, ka, va);
       while (true) {
-        if (base + step >= wend) { compute_rows(uc, base, wbase, wend, ka, va); break; }
+        if (base + step >= wend) { compute_rows(uc, std::false_type{}, base, wbase, wend, ka, va); break; }
         load_rows(uc, base + step, wbase, wend, kb2, vb2);
-        compute_rows(uc, base, wbase, wend, ka, va);
+        compute_rows(uc, std::true_type{}, base, wbase, wend, ka, va);
         base += step;
-        if (base + step >= wend) { compute_rows(uc, base, wbase, wend, kb2, vb2); break; }
+        if (base + step >= wend) { compute_rows(uc, std::false_type{}, base, wbase, wend, kb2, vb2); break; }
         load_rows(uc, base + step, wbase, wend, ka, va);
-        compute_rows(uc, base, wbase, wend, kb2, vb2);
+        compute_rows(uc, std::true_type{}, base, wbase, wend, kb2, vb2);
         base += step;
       }
       return;
     }
     int base = first;
     for (; base + step <= wend; base += step)
-      pass(std::integral_constant<int, U>{}, base, wbase, wend);
+      pass(std::integral_constant<int, U>{}, std::true_type{}, base, wbase, wend);
     if (wend - base > 2 * rows_per_group) {
-      pass(std::integral_constant<int, U>{}, base, wbase, wend);
+      pass(std::integral_constant<int, U>{}, std::false_type{}, base, wbase, wend);
     } else {
       for (; base < wend; base += rows_per_group)
-        pass(std::integral_constant<int, 1>{}, base, wbase, wend);
+        pass(std::integral_constant<int, 1>{}, std::false_type{}, base, wbase, wend);
     }
   };
   if constexpr (MASK) {
