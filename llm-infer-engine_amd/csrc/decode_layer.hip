@@ -29,6 +29,7 @@
 // each).  With the RMSNorm prologue the normalised rows are staged in LDS and
 // the B operands are read from there; otherwise straight from global memory.
 #include <math.h>
+#include <type_traits>
 
 #include "common.hpp"
 
@@ -87,13 +88,27 @@ template <> struct LMfma<f16_t> {
 // 8 signed bytes (two words) -> 8 activation-dtype values (exact).
 template <typename T, typename V8>
 __device__ inline V8 i8x8_cvt(uint32_t lo, uint32_t hi) {
-  V8 r;
+  if constexpr (std::is_same<T, bf16_t>::value) {
+    // integers of magnitude <= 128 have 8 significant bits: the fp32 upper
+    // halves are the bf16 values, so pair them with one byte permute
+    auto hi2 = [](float a, float b) {
+      return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+    };
+    u32x4 r;
+    r.x = hi2((float)(int8_t)lo, (float)(int8_t)(lo >> 8));
+    r.y = hi2((float)(int8_t)(lo >> 16), (float)(int8_t)(lo >> 24));
+    r.z = hi2((float)(int8_t)hi, (float)(int8_t)(hi >> 8));
+    r.w = hi2((float)(int8_t)(hi >> 16), (float)(int8_t)(hi >> 24));
+    return __builtin_bit_cast(V8, r);
+  } else {
+    V8 r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    r[i] = (T)(float)(int8_t)(lo >> (8 * i));
-    r[4 + i] = (T)(float)(int8_t)(hi >> (8 * i));
+    for (int i = 0; i < 4; ++i) {
+      r[i] = (T)(float)(int8_t)(lo >> (8 * i));
+      r[4 + i] = (T)(float)(int8_t)(hi >> (8 * i));
+    }
+    return r;
   }
-  return r;
 }
 
 
