@@ -59,6 +59,7 @@ struct LayerGemvArgs {
   int32_t M, K, N;      // N: output rows (QKV: Hq*D)
   int32_t n_tiles0;     // QKV: tiles of wq (the rest are wk then wv)
   int32_t n_tiles1;
+  int32_t pair_kv;      // QKV with two tiles per block: wk / wv tiles paired too
   // QKV + RoPE + append
   const void* cos;      // [rows, D/2] tables, row stride c_ss (elements); position
   const void* sin;      //   p uses row p - rope_row0
@@ -444,7 +445,7 @@ __global__ __launch_bounds__(64 * NW) void dgemv_kernel(LayerGemvArgs a) {
   constexpr int NMAT = EPI == kEpiSwiglu ? 2 : 1;
   constexpr int NT = NMAT * TPB;                       // 8-row A tiles per block
   constexpr int RB = 8 * TPB;                          // output rows per block (per matrix)
-  constexpr int NOUT = EPI == kEpiQkvRope ? 64 : 8 * RB;  // epilogue threads
+  constexpr int NOUT = EPI == kEpiQkvRope ? 64 * TPB : 8 * RB;  // epilogue threads
   static_assert(NOUT <= 64 * NW, "too few threads for the epilogue");
   __shared__ __align__(16) float red[NT][8][8][NW];    // [tile][row][token][wave]
   __shared__ float ssq[NORM ? NW : 1][8];              // per-wave sums of squares
@@ -460,15 +461,28 @@ __global__ __launch_bounds__(64 * NW) void dgemv_kernel(LayerGemvArgs a) {
   const int ks = (w + (int)blockIdx.x) % NW;
   const int kw = ks * SC * 128;
 
-  // ---- which matrix / tiles this block owns
-  int mat0 = 0, tile0 = blockIdx.x * TPB;
+  // ---- which matrix / tiles this block owns.  QKV: one tile per block, or
+  //      (TPB = 2) tiles 2b and 2b + 1 of wq for the first ceil(n_tiles0 / 2)
+  //      blocks, then the wk and the wv tiles one per block (or in pairs with
+  //      pair_kv).  A CU that runs two blocks streams x twice and sets the
+  //      launch's time, so grids with more tiles than CUs pair them (ntv: the
+  //      tiles this block really has; a missing second tile loads zeros)
+  int mat0 = 0, tile0 = blockIdx.x * TPB, ntv = TPB;
   if constexpr (EPI == kEpiQkvRope) {
-    tile0 = blockIdx.x;
-    if (tile0 >= a.n_tiles0) {
-      tile0 -= a.n_tiles0;
+    int b = blockIdx.x;
+    const int per0 = TPB == 2 ? (a.n_tiles0 + 1) >> 1 : a.n_tiles0;
+    const bool pkv = TPB == 2 && a.pair_kv != 0;
+    const int per1 = pkv ? (a.n_tiles1 + 1) >> 1 : a.n_tiles1;
+    int nt = a.n_tiles0;
+    if (b >= per0) {
+      b -= per0;
       mat0 = 1;
-      if (tile0 >= a.n_tiles1) { tile0 -= a.n_tiles1; mat0 = 2; }
+      if (b >= per1) { b -= per1; mat0 = 2; }
+      nt = a.n_tiles1;
     }
+    const bool paired = TPB == 2 && (mat0 == 0 || pkv);
+    tile0 = paired ? 2 * b : b;
+    ntv = paired ? min(2, nt - tile0) : 1;
   }
   const int half = a.D >> 1, tph = EPI == kEpiQkvRope ? half >> 2 : 1;
   // weight row of tile row `row` of tile `tim` of the matrix: the QKV tiles hold
@@ -494,7 +508,7 @@ __global__ __launch_bounds__(64 * NW) void dgemv_kernel(LayerGemvArgs a) {
   for (int t = 0; t < NT; ++t) {
     const int n = w_row(tile0 + (t % TPB), rr);
     const int64_t sn = t / TPB == 0 ? wsn0 : a.w_sn1;
-    woff[t] = n < nvalid ? (uint32_t)((int64_t)n * sn) : kOobOffset;
+    woff[t] = (n < nvalid && (t % TPB) < ntv) ? (uint32_t)((int64_t)n * sn) : kOobOffset;
   }
 
   // ---- B operand (token rows through a buffer resource: rows >= M read zeros
@@ -534,9 +548,10 @@ __global__ __launch_bounds__(64 * NW) void dgemv_kernel(LayerGemvArgs a) {
   if constexpr (EPI == kEpiQkvRope) {
     pos = *a.pos;
     const T* sc = reinterpret_cast<const T*>(mat0 == 0 ? a.s0 : (mat0 == 1 ? a.s1 : a.s2));
-    const int row = et & 7, j = tile0 % tph;
-    e_s0 = sc[w_row(tile0, row)];
-    e_s1 = sc[w_row(tile0, row ^ 4)];
+    const int tt = tile0 + min(et >> 6, ntv - 1);   // this epilogue thread's tile
+    const int row = et & 7, j = tt % tph;
+    e_s0 = sc[w_row(tt, row)];
+    e_s1 = sc[w_row(tt, row ^ 4)];
     const int64_t crow = min(max(pos - a.rope_row0, (int64_t)0), a.rope_rows - 1);
     const int ii = 4 * j + (row & 3);
     e_cos = reinterpret_cast<const T*>(a.cos)[crow * a.c_ss + ii];
@@ -632,13 +647,14 @@ __global__ __launch_bounds__(64 * NW) void dgemv_kernel(LayerGemvArgs a) {
   auto rnd = [](float v) { return Elem<T>::to_f32(Elem<T>::from_f32(v)); };
 
   if constexpr (EPI == kEpiQkvRope) {
-    const int mm = tid >> 3, row = tid & 7;
-    if (mm >= a.M) return;
-    const float yv = rnd(wsum(0, row, mm) * f32_of(e_s0));
-    const float yp = rnd(wsum(0, row ^ 4, mm) * f32_of(e_s1));
+    const int te = tid >> 6, mm = (tid >> 3) & 7, row = tid & 7;
+    if (mm >= a.M || te >= ntv) return;
+    const int tt = tile0 + te;
+    const float yv = rnd(wsum(te, row, mm) * f32_of(e_s0));
+    const float yp = rnd(wsum(te, row ^ 4, mm) * f32_of(e_s1));
     const bool hi = row >= 4;
-    const int head = tile0 / tph;
-    const int d = w_row(tile0, row) - head * a.D;
+    const int head = tt / tph;
+    const int d = w_row(tt, row) - head * a.D;
     T out;
     if (mat0 == 2) {
       out = Elem<T>::from_f32(yv);                  // v: appended unrotated (bitwise)
@@ -944,9 +960,21 @@ extern "C" int32_t mi_w8a16_qkv_rope_append(
     const int tph = (int)(head_dim / 8);
     a.n_tiles0 = (int32_t)(n_heads * tph);
     a.n_tiles1 = (int32_t)(n_kv_heads * tph);
-    const int n_blocks = a.n_tiles0 + 2 * a.n_tiles1;
-    e = dtype == MI_DTYPE_BF16 ? dispatch_dg<bf16_t, kEpiQkvRope, 1>(a, n_blocks, s)
-                               : dispatch_dg<f16_t, kEpiQkvRope, 1>(a, n_blocks, s);
+    const int n_tiles = a.n_tiles0 + 2 * a.n_tiles1, cus = device_cu_count();
+    if (n_tiles > cus) {
+      // tiles in pairs (see dgemv_kernel): wq's first, and wk's / wv's as well
+      // when that alone leaves more blocks than CUs.  One MI355X, M = 8, K =
+      // 2048, 16-call graph: Llama-3.2-1B (384 tiles -> 256 blocks) 6.34 ->
+      // 5.29 us per call
+      const int per0 = (a.n_tiles0 + 1) / 2;
+      a.pair_kv = per0 + 2 * a.n_tiles1 > cus ? 1 : 0;
+      const int n_blocks = per0 + 2 * (a.pair_kv ? (a.n_tiles1 + 1) / 2 : a.n_tiles1);
+      e = dtype == MI_DTYPE_BF16 ? dispatch_dg<bf16_t, kEpiQkvRope, 2>(a, n_blocks, s)
+                                 : dispatch_dg<f16_t, kEpiQkvRope, 2>(a, n_blocks, s);
+    } else {
+      e = dtype == MI_DTYPE_BF16 ? dispatch_dg<bf16_t, kEpiQkvRope, 1>(a, n_tiles, s)
+                                 : dispatch_dg<f16_t, kEpiQkvRope, 1>(a, n_tiles, s);
+    }
   } else {
     const int tph = (int)(head_dim / 16);   // tiles (8 rotation pairs each) per head
     a.n_tiles0 = (int32_t)(n_heads * tph);
