@@ -149,10 +149,12 @@ def test_unsupported_shapes_are_rejected(dev):
         decode_layer.linear_fused(x3, lin3, lin_b=lin3)
 
 
-def test_qkv_position_outside_cache_writes_nothing(dev):
+# (32, 8): 384 tiles, more than the CUs of an MI355X, so the blocks own two tiles each
+@pytest.mark.parametrize("Hq,Hkv", [(8, 2), (32, 8)])
+def test_qkv_position_outside_cache_writes_nothing(dev, Hq, Hkv):
     from src import decode_layer
     from src.rope import DeviceRopeTable
-    dtype, M, Hq, Hkv, D, dim, T = torch.bfloat16, 4, 8, 2, 64, 512, 64
+    dtype, M, D, dim, T = torch.bfloat16, 4, 64, 512, 64
     attn = _Attn(dev, dim, Hq, Hkv, D, dtype)
     cache = _Cache(dev, 1, M, Hkv, T, D, dtype)
     k0, v0 = cache.k.clone(), cache.v.clone()
