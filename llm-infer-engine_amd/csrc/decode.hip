@@ -93,17 +93,18 @@ DecodePlan make_plan(int32_t dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t 
   p.fused = false;
   // A grid of at most one block per CU leaves each CU one block's waves to
   // hide the round trips: 2-byte K/V with whole-chunk rows then run the
-  // software-pipelined passes with 4 waves per block (two passes of loads in
-  // flight per wave, a 4-wave cross-wave merge).  B8 32/8 D64 at 4097 keys
-  // (256 blocks): 21.1 vs 22.8 us per call; B1 24/8 D128 at 131072 keys,
-  // 16/32 splits (128/256 blocks): 86.3 vs 88.0 us.  With two or more blocks
+  // software-pipelined passes (two passes of loads in flight per wave) with 8
+  // waves per block up to head_dim 64 and 4 above.  B8 32/8 D64 at 4097 keys
+  // (256 blocks): 21.1 vs 22.8 us per call against the single-buffered kernel,
+  // then 19.77 -> 19.65 us with 8 instead of 4 waves; B1 24/8 D128 at 131072
+  // keys, 16/32 splits (128/256 blocks): 86.3 vs 88.0 us, 8 waves no faster.  With two or more blocks
   // per CU the blocks overlap each other and the single-buffered kernel is as
   // fast or faster (B16 24/8 D128, 512 blocks: 69.0 vs 72.2 us; 131072 keys at
   // 64 splits: 88.6 vs 89.6 us).  One MI355X.
   const int64_t blocks = (int64_t)p.n_groups * S;
   const int cus = device_cu_count();
   p.pipe = dtype != MI_DTYPE_F32 && mode == 0 && blocks <= cus;
-  int nw = 4;
+  int nw = p.pipe && D <= 64 ? 8 : 4;
   if (!p.pipe && blocks < cus)
     nw = 16;
   else if (!p.pipe && blocks < 2 * cus)

@@ -24,8 +24,9 @@
 //     matrix tile over, and the loop is HBM-bound;
 //   * grids of at most one block per CU (2-byte K/V, whole-chunk rows) run a
 //     software pipeline over two register sets: the next pass's K/V loads are
-//     in flight while the current pass is folded in (PIPE, 4 waves, 512-thread
-//     register budget); larger grids overlap their blocks instead;
+//     in flight while the current pass is folded in (PIPE: 8 waves up to
+//     head_dim 64, 4 above, 512-thread register budget); larger grids overlap
+//     their blocks instead;
 //   * all splits of one (batch, kv-head) group run on one XCD (the hardware
 //     deals workgroup i to XCD i mod n_xcc), so with an arrival counter the
 //     last split of a group can combine the group's partials from that XCD's
