@@ -25,7 +25,8 @@
 //   * grids of at most one block per CU (2-byte K/V, whole-chunk rows) run a
 //     software pipeline over two register sets: the next pass's K/V loads are
 //     in flight while the current pass is folded in (PIPE: 8 waves up to
-//     head_dim 64, 4 above, 512-thread register budget); larger grids overlap
+//     head_dim 64, 4 above, 512-thread register budget; a last pass whose rows
+//     fit in its first two row slots folds only those); larger grids overlap
 //     their blocks instead;
 //   * all splits of one (batch, kv-head) group run on one XCD (the hardware
 //     deals workgroup i to XCD i mod n_xcc), so with an arrival counter the
@@ -709,14 +710,34 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
       if (first >= wend) return;
       constexpr auto uc = std::integral_constant<int, U>{};
       u32x4 ka[U][CPL], va[U][CPL], kb2[U][CPL], vb2[U][CPL];
+      // the window's last pass: when its rows fit in the first two row slots
+      // (the others hold rows past wend, loaded as zeros), fold only those
+      auto last = [&](const int b0, u32x4 (&kr)[U][CPL], u32x4 (&vr)[U][CPL])
+          __attribute__((always_inline)) {
+        if constexpr (U == 4) {
+          if (wend - b0 <= 2 * rows_per_group) {
+            u32x4 k2[2][CPL], v2[2][CPL];
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+              for (int j = 0; j < CPL; ++j) {
+                k2[u][j] = kr[u][j];
+                v2[u][j] = vr[u][j];
+              }
+            compute_rows(std::integral_constant<int, 2>{}, std::false_type{}, b0, wbase, wend, k2, v2);
+            return;
+          }
+        }
+        compute_rows(uc, std::false_type{}, b0, wbase, wend, kr, vr);
+      };
       int base = first;
       load_rows(uc, base, wbase, wend, ka, va);
       while (true) {
-        if (base + step >= wend) { compute_rows(uc, std::false_type{}, base, wbase, wend, ka, va); break; }
+        if (base + step >= wend) { last(base, ka, va); break; }
         load_rows(uc, base + step, wbase, wend, kb2, vb2);
         compute_rows(uc, std::true_type{}, base, wbase, wend, ka, va);
         base += step;
-        if (base + step >= wend) { compute_rows(uc, std::false_type{}, base, wbase, wend, kb2, vb2); break; }
+        if (base + step >= wend) { last(base, kb2, vb2); break; }
         load_rows(uc, base + step, wbase, wend, ka, va);
         compute_rows(uc, std::true_type{}, base, wbase, wend, kb2, vb2);
         base += step;
