@@ -26,8 +26,8 @@
 //     software pipeline over two register sets: the next pass's K/V loads are
 //     in flight while the current pass is folded in (PIPE: 8 waves up to
 //     head_dim 64, 4 above, 512-thread register budget; a last pass whose rows
-//     fit in its first two row slots folds only those); larger grids overlap
-//     their blocks instead;
+//     fit in its first one or two row slots folds only those); larger grids
+//     overlap their blocks instead;
 //   * all splits of one (batch, kv-head) group run on one XCD (the hardware
 //     deals workgroup i to XCD i mod n_xcc), so with an arrival counter the
 //     last split of a group can combine the group's partials from that XCD's
@@ -710,11 +710,22 @@ __global__ __launch_bounds__((PIPE ? 512 : split_max_threads<T, P, GC, MASK>()))
       if (first >= wend) return;
       constexpr auto uc = std::integral_constant<int, U>{};
       u32x4 ka[U][CPL], va[U][CPL], kb2[U][CPL], vb2[U][CPL];
-      // the window's last pass: when its rows fit in the first two row slots
-      // (the others hold rows past wend, loaded as zeros), fold only those
+      // the window's last pass: when its rows fit in the first one or two row
+      // slots (the others hold rows past wend, loaded as zeros), fold only
+      // those (one slot takes the unpacked P.V: p stays fp32)
       auto last = [&](const int b0, u32x4 (&kr)[U][CPL], u32x4 (&vr)[U][CPL])
           __attribute__((always_inline)) {
         if constexpr (U == 4) {
+          if (wend - b0 <= rows_per_group) {
+            u32x4 k1[1][CPL], v1[1][CPL];
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+              k1[0][j] = kr[0][j];
+              v1[0][j] = vr[0][j];
+            }
+            compute_rows(std::integral_constant<int, 1>{}, std::false_type{}, b0, wbase, wend, k1, v1);
+            return;
+          }
           if (wend - b0 <= 2 * rows_per_group) {
             u32x4 k2[2][CPL], v2[2][CPL];
 #pragma unroll
