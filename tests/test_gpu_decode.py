@@ -364,6 +364,27 @@ def test_decode_element_loads(dev, D, dtype):
         assert max_abs(lse, ref_lse) < LSE_TOL, (D, dtype, kw.keys())
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("path", ["seq_lens", "mask"])
+def test_pipelined_last_pass_lengths(dev, dtype, path):
+    """Config 5's per-layer shape (B8 32/8 D64, 4 splits: one block per CU, the
+    software-pipelined loop, 256 rows per pass).  The sequence lengths leave
+    each split a last pass of one row (L = 1), 16 rows (4097: one row slot),
+    80 (4353: two slots), 144 (4609: a full pass), none (4096: whole passes),
+    240 (4000) and short splits (63, 130); every case against the oracle."""
+    B, Hq, Hkv, D, T, S = 8, 32, 8, 64, 4736, 4
+    q, k, v = _inputs(B, Hq, Hkv, T, D, dtype, dev, seed=41)
+    lens = torch.tensor([4097, 4353, 4609, 4096, 4000, 1, 63, 130])
+    if path == "seq_lens":
+        out, lse = _fd()(q, k, v, num_splits=S, seq_lens=lens.to(dev), return_lse=True)
+    else:
+        mask = (torch.arange(T)[None, :] < lens[:, None]).to(dev)
+        out, lse = _fd()(q, k, v, num_splits=S, mask=mask, return_lse=True)
+    ref, ref_lse = ora.decode(q, k, v, seq_lens=lens)
+    assert max_abs(out, ref) < TOL[dtype], path
+    assert max_abs(lse, ref_lse) < LSE_TOL, path
+
+
 @pytest.mark.parametrize("B,Hq,Hkv,L,D,S", [
     (8, 32, 8, 4097, 64, 4),        # config 5's per-layer shape: in-launch combine
     (2, 8, 2, 999, 128, 8),         # few groups, 8 splits: in-launch combine
