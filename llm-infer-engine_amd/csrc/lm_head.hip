@@ -105,60 +105,6 @@ __global__ __launch_bounds__(64 * kLmWaves) void lm_head_kernel(LmHeadArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // ---- prologue: a = rmsnorm(x) (or x) into LDS, zero row M
-  {
-    const int nch = K / 8;                      // 16-byte chunks per row
-    float ss[16];
-#pragma unroll
-    for (int m = 0; m < 16; ++m) ss[m] = 0.f;
-    for (int m = 0; m < M; ++m) {
-      for (int c = tid; c < nch; c += 64 * kLmWaves) {
-        const u32x4 v = load16(reinterpret_cast<const T*>(a.x) + (int64_t)m * a.x_sm + c * 8);
-        *reinterpret_cast<u32x4*>(xs + m * row_b + c * 16) = v;
-        if (a.norm_w != nullptr) {
-          float f[8];
-          Chunk<T>::unpack(v, f);
-          float t = 0.f;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) t = fmaf(f[e], f[e], t);
-#pragma unroll
-          for (int mm = 0; mm < 16; ++mm)
-            if (mm == m) ss[mm] += t;
-        }
-      }
-    }
-    for (int c = tid; c < nch; c += 64 * kLmWaves)
-      *reinterpret_cast<u32x4*>(xs + M * row_b + c * 16) = u32x4{0, 0, 0, 0};
-    if (a.norm_w != nullptr) {
-#pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        float t = ss[m];
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) t += shfl_xor_f32(t, off);
-        if (lane == 0) red_ss[w][m] = t;
-      }
-    }
-    __syncthreads();
-    if (a.norm_w != nullptr) {
-      for (int m = 0; m < M; ++m) {
-        const float tot = red_ss[0][m] + red_ss[1][m] + red_ss[2][m] + red_ss[3][m];
-        const float rstd = 1.0f / sqrtf(tot / (float)K + a.eps);
-        for (int c = tid; c < nch; c += 64 * kLmWaves) {
-          u32x4* p = reinterpret_cast<u32x4*>(xs + m * row_b + c * 16);
-          float f[8], wn[8];
-          Chunk<T>::unpack(*p, f);
-          Chunk<T>::unpack(load16(reinterpret_cast<const T*>(a.norm_w) + c * 8), wn);
-          typedef T t8 __attribute__((ext_vector_type(8)));
-          t8 o;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[e] = Elem<T>::from_f32(f[e] * rstd * wn[e]);
-          *reinterpret_cast<t8*>(p) = o;
-        }
-      }
-      __syncthreads();
-    }
-  }
-
   // ---- tiles: wave-global index gw walks tiles gw, gw + G, ...
   const int G = gridDim.x * kLmWaves;
   const int gw = blockIdx.x * kLmWaves + w;
@@ -227,9 +173,82 @@ __global__ __launch_bounds__(64 * kLmWaves) void lm_head_kernel(LmHeadArgs a) {
     }
   };
 
+  u32x4 ba[kLmBatch], bb[kLmBatch];
+
+  // ---- prologue: a = rmsnorm(x) (or x) into LDS, zero row M.  The x rows and
+  //      this thread's norm-weight chunks (K <= 4096: at most two) are loaded
+  //      first, then the first weight batch is issued, so the batch streams
+  //      during the statistics and the normalisation (which then wait on LDS
+  //      only, never on a global load issued behind the batch)
+  {
+    const int nch = K / 8;                      // 16-byte chunks per row
+    u32x4 nwr[2] = {u32x4{0, 0, 0, 0}, u32x4{0, 0, 0, 0}};
+    if (a.norm_w != nullptr) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (tid + i * 64 * kLmWaves < nch)
+          nwr[i] = load16(reinterpret_cast<const T*>(a.norm_w) + (tid + i * 64 * kLmWaves) * 8);
+    }
+    float ss[16];
+#pragma unroll
+    for (int m = 0; m < 16; ++m) ss[m] = 0.f;
+    for (int m = 0; m < M; ++m) {
+      for (int c = tid; c < nch; c += 64 * kLmWaves) {
+        const u32x4 v = load16(reinterpret_cast<const T*>(a.x) + (int64_t)m * a.x_sm + c * 8);
+        *reinterpret_cast<u32x4*>(xs + m * row_b + c * 16) = v;
+        if (a.norm_w != nullptr) {
+          float f[8];
+          Chunk<T>::unpack(v, f);
+          float t = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) t = fmaf(f[e], f[e], t);
+#pragma unroll
+          for (int mm = 0; mm < 16; ++mm)
+            if (mm == m) ss[mm] += t;
+        }
+      }
+    }
+    // the norm-weight registers are consumed here (an empty asm taking them),
+    // before the batch is issued, so no later wait on them covers the batch
+    asm volatile("" ::"v"(nwr[0]), "v"(nwr[1]) : "memory");
+    if (n_steps > 0) issue(ba, 0);
+    for (int c = tid; c < nch; c += 64 * kLmWaves)
+      *reinterpret_cast<u32x4*>(xs + M * row_b + c * 16) = u32x4{0, 0, 0, 0};
+    if (a.norm_w != nullptr) {
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        float t = ss[m];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) t += shfl_xor_f32(t, off);
+        if (lane == 0) red_ss[w][m] = t;
+      }
+    }
+    __syncthreads();
+    if (a.norm_w != nullptr) {
+      for (int m = 0; m < M; ++m) {
+        const float tot = red_ss[0][m] + red_ss[1][m] + red_ss[2][m] + red_ss[3][m];
+        const float rstd = 1.0f / sqrtf(tot / (float)K + a.eps);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int c = tid + i * 64 * kLmWaves;
+          if (c >= nch) break;
+          u32x4* p = reinterpret_cast<u32x4*>(xs + m * row_b + c * 16);
+          float f[8];
+          Chunk<T>::unpack(*p, f);
+          typedef T t8 __attribute__((ext_vector_type(8)));
+          t8 o;
+          float wn[8];
+          Chunk<T>::unpack(nwr[i], wn);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = Elem<T>::from_f32(f[e] * rstd * wn[e]);
+          *reinterpret_cast<t8*>(p) = o;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
   if (n_steps > 0) {
-    u32x4 ba[kLmBatch], bb[kLmBatch];
-    issue(ba, 0);
     for (int s = 0; s < n_steps; s += 2) {
       issue(bb, min(s + 1, n_steps - 1));
       compute(ba, s);
