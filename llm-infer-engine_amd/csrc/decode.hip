@@ -97,13 +97,18 @@ DecodePlan make_plan(int32_t dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t 
   // waves per block up to head_dim 64 and 4 above.  B8 32/8 D64 at 4097 keys
   // (256 blocks): 21.1 vs 22.8 us per call against the single-buffered kernel,
   // then 19.77 -> 19.65 us with 8 instead of 4 waves; B1 24/8 D128 at 131072
-  // keys, 16/32 splits (128/256 blocks): 86.3 vs 88.0 us, 8 waves no faster.  With two or more blocks
+  // keys, 16/32 splits (128/256 blocks): 86.3 vs 88.0 us, 8 waves no faster.
+  // Up to two blocks per CU (pipe2) the calls without a mask run the pipelined
+  // kernel too, at 4 waves: B16 24/8 D128 ragged (512 blocks) 69.0 -> 68.0 us,
+  // B1 24/8 D128 131072 keys at 64 splits 87.6 -> 86.4 us; through mask= it
+  // lost (72.8 -> 74.0 us), so mask calls keep the single-buffered kernel there.  With two or more blocks
   // per CU the blocks overlap each other and the single-buffered kernel is as
   // fast or faster (B16 24/8 D128, 512 blocks: 69.0 vs 72.2 us; 131072 keys at
   // 64 splits: 88.6 vs 89.6 us).  One MI355X.
   const int64_t blocks = (int64_t)p.n_groups * S;
   const int cus = device_cu_count();
   p.pipe = dtype != MI_DTYPE_F32 && mode == 0 && blocks <= cus;
+  p.pipe2 = dtype != MI_DTYPE_F32 && mode == 0 && !p.pipe && blocks <= 2 * cus;
   int nw = p.pipe && D <= 64 ? 8 : 4;
   if (!p.pipe && blocks < cus)
     nw = 16;
@@ -114,6 +119,9 @@ DecodePlan make_plan(int32_t dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t 
   if (dtype == MI_DTYPE_F32 && p.P >= 128 && nw > 8) nw = 8;   // split_max_threads
   while (nw > 1 && (int64_t)nw * geo.rpw * geo.u > p.split_len) nw >>= 1;
   p.nw = nw;
+  int nw2 = 4;
+  while (nw2 > 1 && (int64_t)nw2 * geo.rpw * geo.u > p.split_len) nw2 >>= 1;
+  p.nw_pipe2 = nw2;
   return p;
 }
 

@@ -1073,6 +1073,8 @@ struct DecodePlan {
   int P, mode;
   bool fused;   // in-launch combine (MODE 0, no mask; a.arrive set)
   bool pipe;    // software-pipelined passes (2-byte MODE 0; at most 8 waves)
+  bool pipe2;   // two blocks per CU: pipelined passes for calls without a mask
+  int nw_pipe2; // waves per block of those launches
 };
 
 template <typename T, int P, int GC, int MODE>
@@ -1084,8 +1086,9 @@ hipError_t launch_split_t(const DecodeArgs& a, const DecodePlan& p, hipStream_t 
   if constexpr (MODE == 0 && sizeof(T) == 2) {
     // 2-byte K/V with whole-chunk rows: the software-pipelined kernels when
     // the plan asks for them
-    if (!p.pipe) return launch_split_unpiped<T, P, GC, MODE>(a, p, stream);
-    const int nw = min(p.nw, 8);   // built for at most 512 threads
+    const bool piped = p.pipe || (p.pipe2 && a.mask == nullptr);
+    if (!piped) return launch_split_unpiped<T, P, GC, MODE>(a, p, stream);
+    const int nw = min(p.pipe ? p.nw : p.nw_pipe2, 8);   // built for at most 512 threads
     const size_t shmem = (size_t)nw * GC * (P + 2) * sizeof(float);
     const dim3 grid((unsigned)(p.n_groups * S));
     if (a.mask != nullptr) {
