@@ -366,15 +366,18 @@ def test_decode_element_loads(dev, D, dtype):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("path", ["seq_lens", "mask"])
-def test_pipelined_last_pass_lengths(dev, dtype, path):
+@pytest.mark.parametrize("B", [8, 16])
+def test_pipelined_last_pass_lengths(dev, dtype, path, B):
     """Config 5's per-layer shape (B8 32/8 D64, 4 splits: one block per CU, the
-    software-pipelined loop, 256 rows per pass).  The sequence lengths leave
-    each split a last pass of one row (L = 1), 16 rows (4097: one row slot),
+    software-pipelined loop at 8 waves, 256 rows per pass); B16 doubles the
+    grid (two blocks per CU: the pipelined loop at 4 waves for seq_lens, the
+    single-buffered one for the mask).  The sequence lengths leave each split
+    a last pass of one row (L = 1), 16 rows (4097: one row slot at 8 waves),
     80 (4353: two slots), 144 (4609: a full pass), none (4096: whole passes),
     240 (4000) and short splits (63, 130); every case against the oracle."""
-    B, Hq, Hkv, D, T, S = 8, 32, 8, 64, 4736, 4
+    Hq, Hkv, D, T, S = 32, 8, 64, 4736, 4
     q, k, v = _inputs(B, Hq, Hkv, T, D, dtype, dev, seed=41)
-    lens = torch.tensor([4097, 4353, 4609, 4096, 4000, 1, 63, 130])
+    lens = torch.tensor([4097, 4353, 4609, 4096, 4000, 1, 63, 130] * (B // 8))
     if path == "seq_lens":
         out, lse = _fd()(q, k, v, num_splits=S, seq_lens=lens.to(dev), return_lse=True)
     else:
